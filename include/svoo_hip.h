@@ -1,0 +1,163 @@
+/*
+ * svoo_hip.h -- C ABI of the MI355X (gfx950) SVOO online sparse-attention hot path.
+ *
+ * Conventions
+ *   - All tensor arguments are device pointers to contiguous row-major arrays owned by the caller.
+ *     bf16 data is passed as uint16_t bit patterns.  The library never allocates or frees memory;
+ *     entry points that need scratch take (workspace, ws_bytes) sized by the matching
+ *     *_workspace_size() query.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Every entry point only
+ *     enqueues work on that stream and never synchronises the host.
+ *   - Return value: SVOO_OK (0) or a negative SVOO_ERR_* code; svoo_last_error() describes the failure.
+ *   - Shapes use the reference's names: BH = batch*heads, N/S = tokens, D = head dim (128 only),
+ *     QC/KC = query/key cluster counts.
+ *
+ * Reference paths below are relative to the root of the reference repository (Mutual-Luo/SVOO).
+ */
+#ifndef SVOO_HIP_H_
+#define SVOO_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  SVOO_OK = 0,
+  SVOO_ERR_INVALID_ARG = -1,
+  SVOO_ERR_UNSUPPORTED = -2,
+  SVOO_ERR_WORKSPACE = -3,
+  SVOO_ERR_HIP = -4
+};
+
+/* Library version (major*10000 + minor*100 + patch) and last error message of the calling thread. */
+int svoo_version(void);
+const char* svoo_last_error(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Cluster sort: stable counting sort of labels[BH][N] (values in [0, K)).
+ *   sorted_idx[b][s]   original token index at sorted position s (ascending index inside a cluster)
+ *   sizes[b][k]        bincount of the labels
+ *   offsets[b][k]      exclusive prefix of sizes
+ *   sorted_labels      optional (may be NULL): labels[b][sorted_idx[b][s]]
+ * Replaces torch.argsort(labels) in svoo/kernels/triton/permute.py:90 and
+ * torch.sort(cluster_ids) in svoo/co_clustering.py:273-274 (made stable here).
+ * ------------------------------------------------------------------------------------------- */
+size_t svoo_cluster_sort_workspace_size(int bh, int n, int k);
+int svoo_cluster_sort(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
+                      int32_t* offsets, int32_t* sorted_labels, void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Row gather / scatter along the token axis (rows of row_bytes bytes, a multiple of 16).
+ *   svoo_permute_rows:   y[b][s] = x[b][idx[b][s]],  s < n_out, idx values in [0, n_in)
+ *     replaces _permute_kernel / permute_tensor_by_labels_triton, svoo/kernels/triton/permute.py:9-35,68-102
+ *     (also the centroid initialisation gather, svoo/co_clustering.py:2417-2421)
+ *   svoo_permute_rows2:  the same for two tensors sharing one index (K and V, svoo/models/wan/attention.py:1039-1042)
+ *   svoo_unpermute_rows: x[b][idx[b][s]] = y[b][s]
+ *     replaces _inverse_permute_kernel / apply_inverse_permutation_triton, svoo/kernels/triton/permute.py:38-65,105-130
+ *   svoo_unpermute_rows_bshd: the same scatter into the [B, S, H, D] layout (bh = B*H rows of y), i.e.
+ *     apply_inverse_permutation_triton followed by transpose(1, 2).flatten(2, 3) of
+ *     svoo/models/wan/attention.py:1211-1215 in one pass
+ * ------------------------------------------------------------------------------------------- */
+int svoo_permute_rows(const void* x, const int32_t* idx, void* y, int bh, int n_in, int n_out, int row_bytes,
+                      void* stream);
+int svoo_permute_rows2(const void* x0, const void* x1, const int32_t* idx, void* y0, void* y1, int bh, int n,
+                       int row_bytes, void* stream);
+int svoo_unpermute_rows(const void* y, const int32_t* idx, void* x, int bh, int n, int row_bytes, void* stream);
+int svoo_unpermute_rows_bshd(const void* y, const int32_t* idx, void* x, int bh, int n, int heads, int row_bytes,
+                             void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Centroid update over cluster-sorted tokens: new_c[b][k] = bf16(f32(sum of members) / f32(size)),
+ * sizes[b][k] == 0 keeps old_c[b][k].  Sums are exact (fp64), so the result is order independent.
+ * Inputs come from svoo_cluster_sort (sorted_idx, sorted_labels, sizes).  new_c may alias old_c.
+ * Replaces triton_centroid_update_sorted_euclid + _centroid_update_chunk_kernel,
+ * svoo/co_clustering.py:181-303.
+ * ------------------------------------------------------------------------------------------- */
+size_t svoo_centroid_update_workspace_size(int bh, int k, int d);
+int svoo_centroid_update(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
+                         const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k, int d,
+                         void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Row L2 normalisation to fp32: y = x / sqrt(sum(x^2) + eps); x is bf16 (x_is_bf16=1) or fp32.
+ * Replaces triton_l2norm_forward / _l2_norm_fwd_fused, svoo/kernels/triton/l2norm.py:8-80.
+ * ------------------------------------------------------------------------------------------- */
+int svoo_l2norm_rows(const void* x, int x_is_bf16, float* y, long long rows, int cols, float eps, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Co-clustering (profile-space k-means).
+ *   svoo_cocluster_prep: P = l2norm(bf16(A B^T)) ([BH][J][KP], optional output), E = P B split into
+ *     E_hi = bf16(E), E_lo = bf16(E - E_hi), both [BH][jpad][D] with zero rows J..jpad-1.
+ *     Replaces torch.matmul + triton_l2norm_forward, svoo/co_clustering.py:2427-2428,2440-2441.
+ *   svoo_cocluster_assign: labels[b][n] = argmax_j x[b][n] . (E_hi + E_lo)[b][j]  (first j on ties);
+ *     equal to argmin_j 2 - 2 (x C^T / ||x C^T||) . P_j of profile_norm_triton + fused_cocluster_assign_triton,
+ *     svoo/co_clustering.py:2086-2400, because ||x C^T|| > 0 is a per-token constant.
+ *   svoo_co_cluster: max_iters x (key step, query step), all on device, no host synchronisation.
+ *     Replaces co_cluster_tokens, svoo/co_clustering.py:2402-2451.  q_cent / k_cent hold the initial
+ *     centroids on entry and the final ones on return; labels, sizes and the stable sort of the final
+ *     labels (sorted_idx, offsets) are outputs.
+ * ------------------------------------------------------------------------------------------- */
+int svoo_cocluster_prep(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uint16_t* e_lo, float* profile, int bh,
+                        int j, int kp, int d, int jpad, void* stream);
+int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, const uint16_t* e_lo, int32_t* labels, int bh,
+                          int n, int j, int jpad, int d, void* stream);
+size_t svoo_co_cluster_workspace_size(int bh, int n, int qc, int kc, int d);
+int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int n, int d, int qc, int kc, int max_iters,
+                    uint16_t* q_cent, uint16_t* k_cent, int32_t* q_labels, int32_t* k_labels, int32_t* q_sizes,
+                    int32_t* k_sizes, int32_t* q_sorted_idx, int32_t* k_sorted_idx, int32_t* q_offsets,
+                    int32_t* k_offsets, void* workspace, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Block mask: per (b, h, q-cluster) row, weighted softmax of the scaled centroid scores, stable
+ * descending sort, top-p with per-head minimum keep and optional cap, scattered back to a bool map.
+ *   preserve[h], cap[h]: per-head counts computed on the host from min_kc_ratio / max_kc_ratio
+ *   (cap 0 = none); p_storage: top_p rounded to the storage dtype; full != 0 gives an all-true map.
+ *   map[b][h][i][j] (uint8 0/1), lengths[b][h][i] = kept key clusters (may be NULL).
+ * Replaces weighted_softmax + identify_dynamic_map, svoo/co_clustering.py:544-633.
+ * ------------------------------------------------------------------------------------------- */
+int svoo_block_mask(const uint16_t* qc, const uint16_t* kc, const int32_t* k_sizes, const int32_t* preserve,
+                    const int32_t* cap, int b, int h, int qn, int kn, int d, float p_storage, int full, uint8_t* map,
+                    int32_t* lengths, void* stream);
+
+/* Weighted softmax of bf16 scores [rows][cols] with fp32 weights (row stride weight_row_stride, 0 = one
+ * row shared by all) -> bf16 probabilities.
+ * Replaces weighted_softmax, svoo/co_clustering.py:544-553 (fp64 evaluation, rounded via fp32 to bf16). */
+int svoo_weighted_softmax(const uint16_t* scores, const float* weights, long long weight_row_stride,
+                          uint16_t* out, long long rows, int cols, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Variable-block-sparse attention over cluster-contiguous tokens.
+ *   q, k, v, o: [BH][S][D] bf16; map: [BH][QN][KN] uint8; q_sizes [BH][QN], k_sizes [BH][KN] int32.
+ *   For each (b, i): O_i = softmax(Q_i K_S^T / sqrt(D)) V_S over the active key clusters S (ascending),
+ *   fp32 online softmax, bf16 MFMA; rows of a query cluster with no active keys are zero.
+ *   status (device int32, may be NULL) receives 0, or 1 when the sizes of a head do not sum to S
+ *   (that head's output is then left unwritten).
+ * Replaces dynamic_block_sparse_fwd_flashinfer (svoo/co_clustering.py:1231-1311, with the plan of
+ * svoo/utils/flashinfer_sparse.py:43-244) and dynamic_block_sparse_fwd_triton (svoo/co_clustering.py:949-1228).
+ *   svoo_vbsa_segments: the per-(b, i) active key segments (start, length), ascending cluster order,
+ *   that the attention kernel walks: seg_start/seg_len [BH][QN][KN], seg_count [BH][QN].  Expanding them
+ *   gives the reference's kv_indices (svoo/utils/flashinfer_sparse.py:43-97) without the head offset.
+ * ------------------------------------------------------------------------------------------- */
+size_t svoo_vbsa_workspace_size(int bh, int s, int qn, int kn);
+int svoo_vbsa_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint8_t* map,
+                  const int32_t* q_sizes, const int32_t* k_sizes, uint16_t* o, int bh, int s, int d, int qn, int kn,
+                  void* workspace, size_t ws_bytes, int32_t* status, void* stream);
+int svoo_vbsa_segments(const uint8_t* map, const int32_t* k_sizes, int bh, int qn, int kn, int32_t* seg_start,
+                       int32_t* seg_len, int32_t* seg_count, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Diagnostic (no reference counterpart): runs one v_mfma_f32_32x32x16_bf16 and one
+ * v_mfma_f32_16x16x32_bf16 on index-coded operands and writes the raw per-lane accumulators
+ * (out32: 64 lanes x 16 floats, out16: 64 lanes x 4 floats), so tests can confirm the operand
+ * layouts the kernels assume.
+ * ------------------------------------------------------------------------------------------- */
+int svoo_probe_mfma_layout(float* out32, float* out16, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVOO_HIP_H_ */

@@ -1,0 +1,99 @@
+"""ctypes binding of the C ABI in ``include/svoo_hip.h`` (library ``svoo_amd/_svoo_hip.so``).
+
+torch is imported first so that the library's ``libamdhip64.so.7`` dependency resolves to the HIP
+runtime torch already loaded: device pointers and streams are then shared with torch.  There is no
+fallback: if the library is missing or a GPU is absent, calls raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_longlong, c_size_t, c_void_p
+from pathlib import Path
+from typing import Dict, Optional
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+LIB_PATH = Path(__file__).resolve().with_name("_svoo_hip.so")
+
+P = c_void_p
+_SIGS = {
+    "svoo_version": (c_int, []),
+    "svoo_last_error": (ctypes.c_char_p, []),
+    "svoo_cluster_sort_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "svoo_cluster_sort": (c_int, [P, c_int, c_int, c_int, P, P, P, P, P, c_size_t, P]),
+    "svoo_permute_rows": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P]),
+    "svoo_permute_rows2": (c_int, [P, P, P, P, P, c_int, c_int, c_int, P]),
+    "svoo_unpermute_rows": (c_int, [P, P, P, c_int, c_int, c_int, P]),
+    "svoo_unpermute_rows_bshd": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P]),
+    "svoo_centroid_update_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "svoo_centroid_update": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
+    "svoo_l2norm_rows": (c_int, [P, c_int, P, c_longlong, c_int, c_float, P]),
+    "svoo_cocluster_prep": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
+    "svoo_cocluster_assign": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
+    "svoo_co_cluster_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "svoo_co_cluster": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, c_int,
+                                P, P, P, P, P, P, P, P, P, P, P, c_size_t, P]),
+    "svoo_block_mask": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_int, P, P, P]),
+    "svoo_weighted_softmax": (c_int, [P, P, c_longlong, P, c_longlong, c_int, P]),
+    "svoo_vbsa_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "svoo_vbsa_fwd": (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_size_t, P, P]),
+    "svoo_vbsa_segments": (c_int, [P, P, c_int, c_int, c_int, P, P, P, P]),
+    "svoo_probe_mfma_layout": (c_int, [P, P, P]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGS)
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library (once) and declare its signatures."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"SVOO HIP library not found at {LIB_PATH}; build it with "
+                "`python -m svoo_amd.build` (or __graft_entry__.build())"
+            )
+        h = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().svoo_last_error()
+    return msg.decode() if msg else ""
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning entry point; raise ``RuntimeError`` with the library message on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise RuntimeError(f"{name} failed ({rc}): {last_error()}")
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    """Device pointer of a tensor (None -> NULL)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as an integer handle."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu_tensor(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise AssertionError(f"{name} must be a GPU (HIP) tensor")
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Caller-owned scratch from torch's caching allocator (no hipMalloc on the steady state)."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)

@@ -1,0 +1,341 @@
+// Profile-space co-clustering (QK k-means) on device.
+//
+// The reference assigns token x to argmin_j 2 - 2 (x C^T / ||x C^T||) . P_j with P the row-normalised
+// centroid profiles.  ||x C^T|| is a positive per-token constant, so the label is
+// argmax_j x . E_j with E = P C ([J x D]).  That turns the assignment into one [N x D] x [D x J]
+// GEMM with an argmax epilogue, instead of recomputing x C^T for every tile of J.
+//
+// prep:   P = l2norm(bf16(A B^T)) with exact (fp64) dots, E = P B in fp64, split into two bf16
+//         matrices E_hi + E_lo so the bf16 MFMA sees E to ~16 significant bits.
+// assign: 4 waves x 64 tokens per block; token rows stay in registers as the MFMA B operand,
+//         E streams through LDS in 64-row chunks (hi and lo), and each lane keeps a running
+//         argmax over the 16 cluster rows it holds of every 32x32 accumulator tile.
+#include "svoo_common.h"
+
+namespace svoo {
+
+constexpr int kPrepMaxLds = 52 * 1024;  // LDS budget of the prep kernel's profile rows
+constexpr int kAssignChunk = 64;   // E rows staged in LDS per step
+constexpr int kLdsRow = 136;       // bf16 elements per staged row (128 + 8 pad)
+
+// --------------------------------------------------------------------------------------- prep
+// kPrepRows rows of A per block (8 for profile widths up to 1664, else 2, to fit 64 KB of LDS).
+template <int kPrepRows>
+__global__ void __launch_bounds__(256) cocluster_prep_kernel(const uint16_t* __restrict__ a,
+                                                             const uint16_t* __restrict__ bmat,
+                                                             uint16_t* __restrict__ e_hi, uint16_t* __restrict__ e_lo,
+                                                             float* __restrict__ profile, int j, int kp, int jpad) {
+  extern __shared__ unsigned char smem[];
+  double* arow = (double*)smem;                                 // [kPrepRows][128]
+  double* inv = arow + kPrepRows * 128;                         // [kPrepRows]
+  float* praw = (float*)(inv + kPrepRows);                      // [kPrepRows][kp]
+  const int bidx = blockIdx.y;
+  const int r0 = blockIdx.x * kPrepRows;
+  const int tid = threadIdx.x;
+  const uint16_t* ab = a + (size_t)bidx * j * 128;
+  const uint16_t* bb = bmat + (size_t)bidx * kp * 128;
+  const int nrows = max(0, min(kPrepRows, j - r0));
+
+  for (int t = tid; t < kPrepRows * 128; t += 256) {
+    const int r = t / 128, dd = t % 128;
+    arow[t] = (r < nrows) ? (double)bf16_to_f32(ab[(size_t)(r0 + r) * 128 + dd]) : 0.0;
+  }
+  __syncthreads();
+
+  // Phase 1: exact dots A_r . B_k, rounded like a bf16 matmul output (fp32 then bf16).
+  if (nrows > 0) {
+    for (int k = tid; k < kp; k += 256) {
+      double acc[kPrepRows];
+#pragma unroll
+      for (int r = 0; r < kPrepRows; ++r) acc[r] = 0.0;
+      const u32x4_t* brow = (const u32x4_t*)(bb + (size_t)k * 128);
+#pragma unroll 2
+      for (int c = 0; c < 16; ++c) {
+        const u32x4_t w = brow[c];
+        double bv[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          bv[2 * e] = (double)bf16_to_f32((uint16_t)(w[e] & 0xffffu));
+          bv[2 * e + 1] = (double)bf16_to_f32((uint16_t)(w[e] >> 16));
+        }
+#pragma unroll
+        for (int r = 0; r < kPrepRows; ++r) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r] = fma(arow[r * 128 + c * 8 + e], bv[e], acc[r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kPrepRows; ++r) praw[r * kp + k] = bf16_round_f32((float)acc[r]);
+    }
+  }
+  __syncthreads();
+
+  // Phase 2: row norms (one wave per row), inv = 1 / sqrt(sum + 1e-8).
+  const int wave = tid / kWave, lane = tid % kWave;
+  for (int r = wave; r < kPrepRows; r += 4) {
+    double s = 0.0;
+    for (int k = lane; k < kp; k += kWave) {
+      const double v = praw[r * kp + k];
+      s += v * v;
+    }
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    if (lane == 0) inv[r] = 1.0 / sqrt(s + 1e-8);
+  }
+  __syncthreads();
+
+  if (profile) {
+    float* pb = profile + (size_t)bidx * j * kp;
+    for (int t = tid; t < nrows * kp; t += 256) {
+      const int r = t / kp, k = t % kp;
+      pb[(size_t)(r0 + r) * kp + k] = (float)((double)praw[r * kp + k] * inv[r]);
+    }
+  }
+
+  // Phase 3: E[r][dd] = inv_r * sum_k praw[r][k] * B[k][dd] (fp64), split into bf16 hi + lo.
+  const int dd = tid % 128, g = tid / 128;
+  double acc[kPrepRows / 2];
+#pragma unroll
+  for (int q = 0; q < kPrepRows / 2; ++q) acc[q] = 0.0;
+  if (nrows > 0) {
+#pragma unroll 4
+    for (int k = 0; k < kp; ++k) {
+      const double bv = (double)bf16_to_f32(bb[(size_t)k * 128 + dd]);
+#pragma unroll
+      for (int q = 0; q < kPrepRows / 2; ++q) acc[q] = fma((double)praw[(2 * q + g) * kp + k], bv, acc[q]);
+    }
+  }
+  uint16_t* hb = e_hi + (size_t)bidx * jpad * 128;
+  uint16_t* lb = e_lo + (size_t)bidx * jpad * 128;
+#pragma unroll
+  for (int q = 0; q < kPrepRows / 2; ++q) {
+    const int r = 2 * q + g;
+    if (r0 + r >= jpad) continue;
+    uint16_t hi = 0, lo = 0;
+    if (r < nrows) {
+      const double e = acc[q] * inv[r];
+      hi = f32_to_bf16((float)e);
+      lo = f32_to_bf16((float)(e - (double)bf16_to_f32(hi)));
+    }
+    hb[(size_t)(r0 + r) * 128 + dd] = hi;
+    lb[(size_t)(r0 + r) * 128 + dd] = lo;
+  }
+}
+
+// --------------------------------------------------------------------------------------- assign
+__global__ void __launch_bounds__(256) cocluster_assign_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ e_hi,
+                                                               const uint16_t* __restrict__ e_lo,
+                                                               int32_t* __restrict__ labels, int n, int j, int jpad) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_hi[kAssignChunk * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t s_lo[kAssignChunk * kLdsRow];
+  const int bidx = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int h = lane / 32, l32 = lane % 32;
+  const int tok0 = blockIdx.x * 256 + wave * 64;
+  const uint16_t* xb = x + (size_t)bidx * n * 128;
+  const uint16_t* hb = e_hi + (size_t)bidx * jpad * 128;
+  const uint16_t* lb = e_lo + (size_t)bidx * jpad * 128;
+
+  // Token operands: B[k = d][n = token], lane provides 8 consecutive d of token (l32) per k-step.
+  u32x4_t xop[2][8];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int row = min(tok0 + cb * 32 + l32, n - 1);
+    const u32x4_t* src = (const u32x4_t*)(xb + (size_t)row * 128);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) xop[cb][ks] = src[ks * 2 + h];
+  }
+
+  float best_v[2] = {-INFINITY, -INFINITY};
+  int best_j[2] = {0, 0};
+
+  for (int jc = 0; jc < jpad; jc += kAssignChunk) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 256 * i;  // 1024 16-byte pieces per matrix
+      const int row = c / 16, part = c % 16;
+      const u32x4_t vh = ((const u32x4_t*)(hb + (size_t)(jc + row) * 128))[part];
+      const u32x4_t vl = ((const u32x4_t*)(lb + (size_t)(jc + row) * 128))[part];
+      *(u32x4_t*)(&s_hi[row * kLdsRow + part * 8]) = vh;
+      *(u32x4_t*)(&s_lo[row * kLdsRow + part * 8]) = vl;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < kAssignChunk / 32; ++rb) {
+      f32x16_t acc[2] = {};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const int off = (rb * 32 + l32) * kLdsRow + ks * 16 + h * 8;
+        const bf16x8_t ah = as_bf16x8(*(const u32x4_t*)(&s_hi[off]));
+        const bf16x8_t al = as_bf16x8(*(const u32x4_t*)(&s_lo[off]));
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          acc[cb] = mfma32x32x16(ah, as_bf16x8(xop[cb][ks]), acc[cb]);
+          acc[cb] = mfma32x32x16(al, as_bf16x8(xop[cb][ks]), acc[cb]);
+        }
+      }
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int jj = jc + rb * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+          const float v = acc[cb][r];
+          if (jj < j && v > best_v[cb]) {
+            best_v[cb] = v;
+            best_j[cb] = jj;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const float ov = __shfl_xor(best_v[cb], 32);
+    const int oj = __shfl_xor(best_j[cb], 32);
+    if (ov > best_v[cb] || (ov == best_v[cb] && oj < best_j[cb])) {
+      best_v[cb] = ov;
+      best_j[cb] = oj;
+    }
+    const int tok = tok0 + cb * 32 + l32;
+    if (h == 0 && tok < n) labels[(size_t)bidx * n + tok] = best_j[cb];
+  }
+}
+
+}  // namespace svoo
+
+using namespace svoo;
+
+// Forward declarations of the other translation units' internal entry points.
+int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
+                           int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
+                           hipStream_t stream);
+int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
+                              const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
+                              double* sums, hipStream_t stream);
+int svoo_zero_f64(double* p, long long n, hipStream_t stream);
+
+static inline int pad_to(int v, int m) { return (v + m - 1) / m * m; }
+
+static size_t prep_smem(int rows, int kp) {
+  return (size_t)rows * 128 * sizeof(double) + rows * sizeof(double) + (size_t)rows * kp * sizeof(float);
+}
+
+static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uint16_t* e_lo, float* profile, int bh,
+                       int j, int kp, int jpad, hipStream_t stream) {
+  if ((size_t)8 * kp * sizeof(float) <= (size_t)kPrepMaxLds) {
+    hipLaunchKernelGGL(cocluster_prep_kernel<8>, dim3(jpad / 8, bh), dim3(256), prep_smem(8, kp), stream, a, b, e_hi,
+                       e_lo, profile, j, kp, jpad);
+  } else {
+    hipLaunchKernelGGL(cocluster_prep_kernel<2>, dim3(jpad / 2, bh), dim3(256), prep_smem(2, kp), stream, a, b, e_hi,
+                       e_lo, profile, j, kp, jpad);
+  }
+  return check_launch("svoo_cocluster_prep");
+}
+
+static int assign_launch(const uint16_t* x, const uint16_t* e_hi, const uint16_t* e_lo, int32_t* labels, int bh, int n,
+                         int j, int jpad, hipStream_t stream) {
+  dim3 grid((n + 255) / 256, bh);
+  hipLaunchKernelGGL(cocluster_assign_kernel, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad);
+  return check_launch("svoo_cocluster_assign");
+}
+
+static const int kMaxClusters = 4096;
+
+extern "C" int svoo_cocluster_prep(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uint16_t* e_lo,
+                                   float* profile, int bh, int j, int kp, int d, int jpad, void* stream) {
+  SVOO_REQUIRE(a && b && e_hi && e_lo, SVOO_ERR_INVALID_ARG, "svoo_cocluster_prep: null pointer");
+  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_cocluster_prep: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE(bh > 0 && bh <= 65535 && j > 0 && kp > 0, SVOO_ERR_INVALID_ARG, "svoo_cocluster_prep: bad dims");
+  SVOO_REQUIRE(j <= kMaxClusters && kp <= kMaxClusters, SVOO_ERR_UNSUPPORTED,
+               "svoo_cocluster_prep: cluster counts above %d", kMaxClusters);
+  SVOO_REQUIRE(jpad >= j && jpad % kAssignChunk == 0, SVOO_ERR_INVALID_ARG,
+               "svoo_cocluster_prep: jpad=%d must be >= j and a multiple of %d", jpad, kAssignChunk);
+  return prep_launch(a, b, e_hi, e_lo, profile, bh, j, kp, jpad, (hipStream_t)stream);
+}
+
+extern "C" int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, const uint16_t* e_lo, int32_t* labels,
+                                     int bh, int n, int j, int jpad, int d, void* stream) {
+  SVOO_REQUIRE(x && e_hi && e_lo && labels, SVOO_ERR_INVALID_ARG, "svoo_cocluster_assign: null pointer");
+  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_cocluster_assign: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE(bh > 0 && bh <= 65535 && n > 0 && j > 0, SVOO_ERR_INVALID_ARG, "svoo_cocluster_assign: bad dims");
+  SVOO_REQUIRE(jpad >= j && jpad % kAssignChunk == 0, SVOO_ERR_INVALID_ARG,
+               "svoo_cocluster_assign: jpad=%d must be >= j and a multiple of %d", jpad, kAssignChunk);
+  return assign_launch(x, e_hi, e_lo, labels, bh, n, j, jpad, (hipStream_t)stream);
+}
+
+// Workspace layout of svoo_co_cluster (each region 256-byte aligned):
+//   e_hi, e_lo   [bh][jpad_max][128] bf16
+//   counts       [bh][kmax][nchunks] int32   (cluster-sort scratch)
+//   sums         [bh][kmax][128] fp64        (centroid sums, kept zero between uses)
+//   sorted_lab   [bh][n] int32
+struct CoClusterWs {
+  size_t e_off, counts_off, sums_off, slab_off, total;
+};
+
+static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
+  auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+  const int kmax = qc > kc ? qc : kc;
+  const int jpad = pad_to(kmax, kAssignChunk);
+  const int nch = (n + 1023) / 1024;
+  CoClusterWs w;
+  w.e_off = 0;
+  size_t e_bytes = al((size_t)bh * jpad * 128 * sizeof(uint16_t));
+  w.counts_off = 2 * e_bytes;
+  w.sums_off = w.counts_off + al((size_t)bh * kmax * nch * sizeof(int32_t));
+  w.slab_off = w.sums_off + al((size_t)bh * kmax * 128 * sizeof(double));
+  w.total = w.slab_off + al((size_t)bh * n * sizeof(int32_t));
+  return w;
+}
+
+extern "C" size_t svoo_co_cluster_workspace_size(int bh, int n, int qc, int kc, int d) {
+  (void)d;
+  if (bh <= 0 || n <= 0 || qc <= 0 || kc <= 0) return 256;
+  return co_cluster_layout(bh, n, qc, kc).total;
+}
+
+extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int n, int d, int qc, int kc,
+                               int max_iters, uint16_t* q_cent, uint16_t* k_cent, int32_t* q_labels,
+                               int32_t* k_labels, int32_t* q_sizes, int32_t* k_sizes, int32_t* q_sorted_idx,
+                               int32_t* k_sorted_idx, int32_t* q_offsets, int32_t* k_offsets, void* workspace,
+                               size_t ws_bytes, void* stream) {
+  SVOO_REQUIRE(q && k && q_cent && k_cent && q_labels && k_labels && q_sizes && k_sizes && q_sorted_idx &&
+                   k_sorted_idx && q_offsets && k_offsets,
+               SVOO_ERR_INVALID_ARG, "svoo_co_cluster: null pointer");
+  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_co_cluster: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE(bh > 0 && bh <= 65535 && n > 0 && qc > 0 && kc > 0, SVOO_ERR_INVALID_ARG,
+               "svoo_co_cluster: bad dims bh=%d n=%d qc=%d kc=%d", bh, n, qc, kc);
+  SVOO_REQUIRE(qc <= kMaxClusters && kc <= kMaxClusters, SVOO_ERR_UNSUPPORTED,
+               "svoo_co_cluster: cluster counts above %d", kMaxClusters);
+  SVOO_REQUIRE(max_iters >= 1, SVOO_ERR_INVALID_ARG, "svoo_co_cluster: max_iters=%d must be >= 1", max_iters);
+  SVOO_REQUIRE((long long)bh * n * 128 < (1ll << 40), SVOO_ERR_UNSUPPORTED, "svoo_co_cluster: too large");
+  const CoClusterWs lay = co_cluster_layout(bh, n, qc, kc);
+  SVOO_REQUIRE(workspace && ws_bytes >= lay.total, SVOO_ERR_WORKSPACE, "svoo_co_cluster: workspace %zu < %zu",
+               ws_bytes, lay.total);
+  hipStream_t s = (hipStream_t)stream;
+  char* base = (char*)workspace;
+  const size_t e_bytes = (lay.counts_off) / 2;
+  uint16_t* e_hi = (uint16_t*)(base + lay.e_off);
+  uint16_t* e_lo = (uint16_t*)(base + lay.e_off + e_bytes);
+  int32_t* counts = (int32_t*)(base + lay.counts_off);
+  double* sums = (double*)(base + lay.sums_off);
+  int32_t* slab = (int32_t*)(base + lay.slab_off);
+  const int kmax = qc > kc ? qc : kc;
+  const int jpad_k = pad_to(kc, kAssignChunk), jpad_q = pad_to(qc, kAssignChunk);
+  int rc = svoo_zero_f64(sums, (long long)bh * kmax * 128, s);
+  for (int it = 0; it < max_iters && rc == SVOO_OK; ++it) {
+    // Key step: profiles of keys live in query-centroid space.
+    if ((rc = prep_launch(k_cent, q_cent, e_hi, e_lo, nullptr, bh, kc, qc, jpad_k, s))) break;
+    if ((rc = assign_launch(k, e_hi, e_lo, k_labels, bh, n, kc, jpad_k, s))) break;
+    if ((rc = svoo_cluster_sort_impl(k_labels, bh, n, kc, k_sorted_idx, k_sizes, k_offsets, slab, counts, nullptr, s)))
+      break;
+    if ((rc = svoo_centroid_update_impl(k, k_sorted_idx, slab, k_sizes, k_cent, k_cent, bh, n, kc, sums, s))) break;
+    // Query step: profiles of queries live in the space of the new key centroids.
+    if ((rc = prep_launch(q_cent, k_cent, e_hi, e_lo, nullptr, bh, qc, kc, jpad_q, s))) break;
+    if ((rc = assign_launch(q, e_hi, e_lo, q_labels, bh, n, qc, jpad_q, s))) break;
+    if ((rc = svoo_cluster_sort_impl(q_labels, bh, n, qc, q_sorted_idx, q_sizes, q_offsets, slab, counts, nullptr, s)))
+      break;
+    if ((rc = svoo_centroid_update_impl(q, q_sorted_idx, slab, q_sizes, q_cent, q_cent, bh, n, qc, sums, s))) break;
+  }
+  return rc;
+}

@@ -1,0 +1,144 @@
+// Stable counting sort of cluster labels (per batch-head row).
+//
+// Three HBM-light passes over labels[BH][N] (int32):
+//   1. hist:    per 1024-token chunk, an LDS histogram -> counts[b][k][chunk]   (cluster-major)
+//   2. scan:    per row, exclusive scan of counts in (cluster, chunk) order      -> chunk bases,
+//               sizes[b][k] and offsets[b][k]
+//   3. scatter: one wave per chunk walks its tokens in order, 64 at a time; lanes with the same
+//               label are ranked by lane order (ballot + popcount), so equal labels keep their
+//               original token order (stable).
+#include "svoo_common.h"
+
+namespace svoo {
+
+constexpr int kSortChunk = 1024;
+constexpr int kMaxSortClusters = 16384;
+
+__global__ void __launch_bounds__(256) sort_hist_kernel(const int32_t* __restrict__ labels, int n, int k,
+                                                        int nchunks, int32_t* __restrict__ counts,
+                                                        int32_t* __restrict__ err) {
+  extern __shared__ int32_t hist[];
+  const int b = blockIdx.y, c = blockIdx.x;
+  for (int i = threadIdx.x; i < k; i += blockDim.x) hist[i] = 0;
+  __syncthreads();
+  const int32_t* lab = labels + (size_t)b * n;
+  const int s = c * kSortChunk, e = min(n, s + kSortChunk);
+  bool bad = false;
+  for (int t = s + threadIdx.x; t < e; t += blockDim.x) {
+    const int l = lab[t];
+    if ((unsigned)l < (unsigned)k)
+      atomicAdd(&hist[l], 1);
+    else
+      bad = true;
+  }
+  if (bad && err) atomicOr(err, 1);
+  __syncthreads();
+  int32_t* out = counts + (size_t)b * k * nchunks;
+  for (int i = threadIdx.x; i < k; i += blockDim.x) out[(size_t)i * nchunks + c] = hist[i];
+}
+
+__global__ void __launch_bounds__(1024) sort_scan_kernel(int32_t* __restrict__ counts, int k, int nchunks,
+                                                         int32_t* __restrict__ sizes, int32_t* __restrict__ offsets) {
+  __shared__ long long scratch[1024 / kWave];
+  const int b = blockIdx.x;
+  int32_t* cnt = counts + (size_t)b * k * nchunks;
+  const long long total = (long long)k * nchunks;
+  const long long per = (total + blockDim.x - 1) / blockDim.x;
+  const long long s = min(total, per * threadIdx.x), e = min(total, s + per);
+  long long local = 0;
+  for (long long i = s; i < e; ++i) local += cnt[i];
+  long long all;
+  long long run = block_exclusive_scan_i64<1024>(local, scratch, &all);
+  for (long long i = s; i < e; ++i) {
+    const int32_t v = cnt[i];
+    cnt[i] = (int32_t)run;
+    run += v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < k; i += blockDim.x) {
+    const int32_t start = cnt[(size_t)i * nchunks];
+    const int32_t next = (i + 1 < k) ? cnt[(size_t)(i + 1) * nchunks] : (int32_t)all;
+    offsets[(size_t)b * k + i] = start;
+    sizes[(size_t)b * k + i] = next - start;
+  }
+}
+
+__global__ void __launch_bounds__(64) sort_scatter_kernel(const int32_t* __restrict__ labels, int n, int k,
+                                                          int nchunks, const int32_t* __restrict__ bases,
+                                                          int32_t* __restrict__ sorted_idx,
+                                                          int32_t* __restrict__ sorted_labels) {
+  extern __shared__ int32_t base[];
+  const int b = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
+  const int32_t* bs = bases + (size_t)b * k * nchunks;
+  for (int i = lane; i < k; i += kWave) base[i] = bs[(size_t)i * nchunks + c];
+  __syncthreads();
+  const int32_t* lab = labels + (size_t)b * n;
+  int32_t* out = sorted_idx + (size_t)b * n;
+  int32_t* outl = sorted_labels ? sorted_labels + (size_t)b * n : nullptr;
+  const int s = c * kSortChunk, e = min(n, s + kSortChunk);
+  const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int t0 = s; t0 < e; t0 += kWave) {
+    const int t = t0 + lane;
+    const bool valid = t < e;
+    int l = valid ? lab[t] : -1;
+    if ((unsigned)l >= (unsigned)k) l = -1;  // out-of-range labels were flagged by the hist pass
+    unsigned long long pending = __ballot(l >= 0);
+    while (pending) {
+      const int leader = __ffsll((long long)pending) - 1;
+      const int ll = __shfl(l, leader);
+      const unsigned long long same = __ballot(l == ll) & pending;
+      const int bval = base[ll];
+      if (l == ll) {
+        const int pos = bval + __popcll(same & below);
+        if ((unsigned)pos < (unsigned)n) {  // always true for consistent bases; guards memory anyway
+          out[pos] = t;
+          if (outl) outl[pos] = ll;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (lane == leader) base[ll] = bval + __popcll(same);
+      __builtin_amdgcn_wave_barrier();
+      pending &= ~same;
+    }
+  }
+}
+
+}  // namespace svoo
+
+using namespace svoo;
+
+static inline int sort_nchunks(int n) { return (n + kSortChunk - 1) / kSortChunk; }
+
+extern "C" size_t svoo_cluster_sort_workspace_size(int bh, int n, int k) {
+  if (bh <= 0 || n <= 0 || k <= 0) return 256;
+  return ((size_t)bh * k * sort_nchunks(n) * sizeof(int32_t) + 255) / 256 * 256 + 256;
+}
+
+// Internal entry used by the co-clustering driver: the workspace pointer is already sized.
+int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
+                           int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
+                           hipStream_t stream) {
+  const int nch = sort_nchunks(n);
+  hipLaunchKernelGGL(sort_hist_kernel, dim3(nch, bh), dim3(256), k * sizeof(int32_t), stream, labels, n, k, nch,
+                     counts, err);
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(bh), dim3(1024), 0, stream, counts, k, nch, sizes, offsets);
+  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nch, bh), dim3(64), k * sizeof(int32_t), stream, labels, n, k, nch,
+                     counts, sorted_idx, sorted_labels);
+  return check_launch("svoo_cluster_sort");
+}
+
+extern "C" int svoo_cluster_sort(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
+                                 int32_t* offsets, int32_t* sorted_labels, void* workspace, size_t ws_bytes,
+                                 void* stream) {
+  SVOO_REQUIRE(labels && sorted_idx && sizes && offsets, SVOO_ERR_INVALID_ARG, "svoo_cluster_sort: null pointer");
+  SVOO_REQUIRE(bh > 0 && n > 0 && k > 0, SVOO_ERR_INVALID_ARG, "svoo_cluster_sort: bad dims bh=%d n=%d k=%d", bh,
+               n, k);
+  SVOO_REQUIRE(k <= kMaxSortClusters, SVOO_ERR_UNSUPPORTED, "svoo_cluster_sort: k=%d exceeds %d", k,
+               kMaxSortClusters);
+  SVOO_REQUIRE((long long)bh * n < (1ll << 31), SVOO_ERR_UNSUPPORTED, "svoo_cluster_sort: bh*n too large");
+  const size_t need = svoo_cluster_sort_workspace_size(bh, n, k);
+  SVOO_REQUIRE(workspace && ws_bytes >= need, SVOO_ERR_WORKSPACE, "svoo_cluster_sort: workspace %zu < %zu",
+               ws_bytes, need);
+  return svoo_cluster_sort_impl(labels, bh, n, k, sorted_idx, sizes, offsets, sorted_labels, (int32_t*)workspace,
+                                nullptr, (hipStream_t)stream);
+}

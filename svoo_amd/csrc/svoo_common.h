@@ -1,0 +1,125 @@
+// Shared device helpers and host error plumbing for the SVOO HIP kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/svoo_hip.h"
+
+namespace svoo {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 <-> f32
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// Round-to-nearest-even float32 -> bfloat16 bit pattern (NaN -> quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)0x7fc0u;
+  uint32_t lsb = (u >> 16) & 1u;
+  return (uint16_t)((u + 0x7fffu + lsb) >> 16);
+}
+
+__device__ __forceinline__ float bf16_round_f32(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ---------------------------------------------------------------- vector types for MFMA
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// 32x32x16 bf16 MFMA, fp32 accumulate.  Operand layout (wave64):
+//   A[m][k]: lane m + 32*(k/8), element k%8     B[k][n]: lane n + 32*(k/8), element k%8
+//   C[m][n]: lane n + 32*((m/4)%2), element (m/8)*4 + m%4
+__device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// 16x16x32 bf16 MFMA.  A[m][k]: lane m + 16*(k/8); C[m][n]: lane n + 16*(m/4), element m%4.
+__device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// ---------------------------------------------------------------- block reductions
+template <int kThreads>
+__device__ __forceinline__ double block_sum_f64(double v, double* scratch) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  __syncthreads();
+  if (l == 0) scratch[w] = v;
+  __syncthreads();
+  double t = 0.0;
+#pragma unroll
+  for (int i = 0; i < kThreads / kWave; ++i) t += scratch[i];
+  return t;
+}
+
+template <int kThreads>
+__device__ __forceinline__ float block_max_f32(float v, float* scratch) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  __syncthreads();
+  if (l == 0) scratch[w] = v;
+  __syncthreads();
+  float t = scratch[0];
+#pragma unroll
+  for (int i = 1; i < kThreads / kWave; ++i) t = fmaxf(t, scratch[i]);
+  return t;
+}
+
+template <int kThreads>
+__device__ __forceinline__ int block_sum_i32(int v, int* scratch) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  __syncthreads();
+  if (l == 0) scratch[w] = v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int i = 0; i < kThreads / kWave; ++i) t += scratch[i];
+  return t;
+}
+
+// Exclusive prefix sum over the block (int64); returns this thread's exclusive prefix and writes the total.
+template <int kThreads>
+__device__ __forceinline__ long long block_exclusive_scan_i64(long long v, long long* scratch, long long* total) {
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  long long inc = v;
+  for (int o = 1; o < kWave; o <<= 1) {
+    long long n = __shfl_up(inc, o);
+    if (l >= o) inc += n;
+  }
+  __syncthreads();
+  if (l == kWave - 1) scratch[w] = inc;
+  __syncthreads();
+  long long base = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kThreads / kWave; ++i) {
+    if (i < w) base += scratch[i];
+    tot += scratch[i];
+  }
+  *total = tot;
+  return base + inc - v;
+}
+
+// ---------------------------------------------------------------- host side
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+
+}  // namespace svoo
+
+#define SVOO_REQUIRE(cond, code, ...)     \
+  do {                                    \
+    if (!(cond)) {                        \
+      ::svoo::set_error(__VA_ARGS__);     \
+      return (code);                      \
+    }                                     \
+  } while (0)

@@ -1,0 +1,305 @@
+"""GPU parity of every HIP kernel against the oracle (bit-exact for integer/index/mask work,
+tolerance-bounded for floating point).  Each test prints the case it runs before launching."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import svoo_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ATTN_MAX_ABS = 2e-2  # bf16 attention tolerance (max-abs) from the north-star contract
+ATTN_MIN_COS = 0.999
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def bf16(x_np, dev):
+    return torch.from_numpy(np.ascontiguousarray(x_np, dtype=np.float32)).to(torch.bfloat16).to(dev)
+
+
+def f32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def rand_bf16(shape, seed, dev, scale=1.0):
+    r = np.random.default_rng(seed)
+    x = O.bf16_round((r.standard_normal(shape) * scale).astype(np.float32))
+    return x, bf16(x, dev)
+
+
+def test_mfma_operand_layout(gpu):
+    from svoo_amd import _lib
+
+    say("mfma layout probe")
+    o32 = torch.zeros(64 * 16, dtype=torch.float32, device=gpu)
+    o16 = torch.zeros(64 * 4, dtype=torch.float32, device=gpu)
+    _lib.call("svoo_probe_mfma_layout", o32.data_ptr(), o16.data_ptr(), _lib.stream_of(gpu))
+    torch.cuda.synchronize()
+    c32 = o32.cpu().numpy().reshape(64, 16)
+    c16 = o16.cpu().numpy().reshape(64, 4)
+    for l in range(64):
+        for r in range(16):
+            m, n = (r // 4) * 8 + (l // 32) * 4 + r % 4, l % 32
+            assert c32[l, r] == 64 * m + n, (l, r, c32[l, r])
+        for r in range(4):
+            m, n = 4 * (l // 16) + r, l % 16
+            assert c16[l, r] == 16 * m + n, (l, r, c16[l, r])
+
+
+@pytest.mark.parametrize("bh,n,k", [(3, 5000, 37), (2, 1024, 1), (1, 1, 1), (2, 777, 2000), (4, 2049, 1000)])
+def test_cluster_sort_bit_exact(gpu, bh, n, k):
+    from svoo_amd.permute import cluster_sort
+
+    say("cluster_sort", bh, n, k)
+    r = np.random.default_rng(n + k)
+    labels = r.integers(0, k, size=(bh, n))
+    idx, sizes, offs, slab = cluster_sort(torch.from_numpy(labels).to(gpu), k, with_sorted_labels=True)
+    oidx, osz, ooff = O.cluster_sort(labels, k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+    np.testing.assert_array_equal(sizes.cpu().numpy(), osz)
+    np.testing.assert_array_equal(offs.cpu().numpy(), ooff)
+    np.testing.assert_array_equal(slab.cpu().numpy(), np.take_along_axis(labels, oidx.astype(np.int64), 1))
+
+
+def test_permute_unpermute_bit_exact(gpu):
+    from svoo_amd.permute import (apply_inverse_permutation, apply_inverse_permutation_bshd,
+                                  permute_pair_by_indices, permute_tensor_by_labels)
+
+    say("permute 1x3x3001x128")
+    x, xt = rand_bf16((1, 3, 3001, 128), 1, gpu)
+    v, vt = rand_bf16((1, 3, 3001, 128), 2, gpu)
+    labels = np.random.default_rng(3).integers(0, 50, size=(3, 3001))
+    y, idx = permute_tensor_by_labels(xt, torch.from_numpy(labels).to(gpu), 2)
+    oidx, _, _ = O.cluster_sort(labels, 50)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+    np.testing.assert_array_equal(f32(y)[0], O.permute_rows(x[0], oidx))
+    ky, vy = permute_pair_by_indices(xt, vt, idx)
+    assert torch.equal(ky, y)
+    np.testing.assert_array_equal(f32(vy)[0], O.permute_rows(v[0], oidx))
+    back = apply_inverse_permutation(y, idx, 2)
+    assert torch.equal(back, xt)
+    bshd = apply_inverse_permutation_bshd(y, idx)
+    assert torch.equal(bshd, xt.transpose(1, 2).flatten(2, 3))
+    # given sorted indices, labels are ignored
+    y2, idx2 = permute_tensor_by_labels(xt, None, 2, sorted_indices=idx)
+    assert torch.equal(y2, y) and torch.equal(idx2, idx)
+
+
+def test_centroid_update_bit_exact(gpu):
+    from svoo_amd.co_clustering import centroid_update
+
+    for bh, n, k in [(2, 3000, 100), (3, 700, 1000), (1, 64, 3)]:
+        say("centroid_update", bh, n, k)
+        x, xt = rand_bf16((bh, n, 128), n, gpu, scale=2.0)
+        old, oldt = rand_bf16((bh, k, 128), k, gpu)
+        labels = np.random.default_rng(7).integers(0, k, size=(bh, n))
+        labels[0][labels[0] == 1] = 0  # cluster 1 empty in row 0
+        new, cnt = centroid_update(xt, torch.from_numpy(labels).to(gpu), oldt)
+        onew, ocnt = O.centroid_update(x, labels, old)
+        np.testing.assert_array_equal(cnt.cpu().numpy(), ocnt)
+        np.testing.assert_array_equal(f32(new), onew)
+
+
+def test_l2norm(gpu):
+    from svoo_amd.co_clustering import triton_l2norm_forward
+
+    say("l2norm")
+    x, xt = rand_bf16((3, 100, 1000), 5, gpu)
+    y = triton_l2norm_forward(xt, 1e-8)
+    np.testing.assert_allclose(f32(y), O.l2norm_rows(x), rtol=2e-6, atol=1e-7)
+
+
+def test_profile_prep(gpu):
+    from svoo_amd.co_clustering import cocluster_profile
+
+    for j, kp in [(1000, 100), (100, 1000), (70, 33), (5, 1800)]:
+        say("cocluster_prep", j, kp)
+        a, at = rand_bf16((2, j, 128), j, gpu)
+        b, btt = rand_bf16((2, kp, 128), kp + 1, gpu)
+        prof, e_hi, e_lo = cocluster_profile(at, btt)
+        ref = O.profile_centroids(a, b)
+        np.testing.assert_allclose(f32(prof), ref, rtol=1e-6, atol=1e-7)
+        e = (e_hi.double() + e_lo.double()).cpu().numpy()[:, :j]
+        e_ref = ref @ b.astype(np.float64)
+        scale = np.abs(e_ref).max()
+        assert np.abs(e - e_ref).max() <= 3e-5 * scale
+        assert torch.all(e_hi[:, j:] == 0) and torch.all(e_lo[:, j:] == 0)
+
+
+def test_assign_matches_literal_argmin(gpu):
+    from svoo_amd.co_clustering import cocluster_assign
+
+    for n, j, kp in [(5000, 1000, 100), (4000, 100, 1000), (333, 7, 5)]:
+        say("cocluster_assign", n, j, kp)
+        x, xt = rand_bf16((2, n, 128), n, gpu)
+        cent, ct = rand_bf16((2, j, 128), j + 7, gpu)
+        basis, bt = rand_bf16((2, kp, 128), kp + 9, gpu)
+        lab = cocluster_assign(xt, ct, bt).cpu().numpy()
+        ref, margin = O.cocluster_assign(x, basis, O.profile_centroids(cent, basis))
+        diff = lab != ref
+        # a mismatch is allowed only at a near-tie of the literal distance
+        assert np.all(margin[diff] < 1e-4), (diff.sum(), margin[diff].max() if diff.any() else None)
+        assert diff.mean() < 1e-3
+
+
+def test_weighted_softmax_bit_exact(gpu):
+    from svoo_amd.co_clustering import weighted_softmax
+
+    say("weighted_softmax")
+    s, st = rand_bf16((2, 3, 7, 1000), 11, gpu, scale=3.0)
+    w = np.random.default_rng(12).integers(0, 200, size=(2, 3, 1, 1000)).astype(np.float32)
+    out = weighted_softmax(st, torch.from_numpy(w).to(gpu))
+    ref = O.weighted_softmax(s, np.broadcast_to(w, s.shape))
+    np.testing.assert_array_equal(f32(out), ref)
+
+
+def _mask_case(gpu, h, qn, kn, seed):
+    r = np.random.default_rng(seed)
+    qc = O.bf16_round((r.standard_normal((1, h, qn, 128)) * 0.5).astype(np.float32))
+    kc = O.bf16_round((r.standard_normal((1, h, kn, 128)) * 0.5).astype(np.float32))
+    qs = r.integers(1, 400, size=(1, h, qn)).astype(np.int32)
+    ks = r.integers(0, 200, size=(1, h, kn)).astype(np.int32)
+    return (qc, kc, qs, ks), (bf16(qc, gpu), bf16(kc, gpu), torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu))
+
+
+@pytest.mark.parametrize("p,mn,mx", [
+    (0.9, [0.15, 0.2, 0.18], 0), (0.0, [0.05, 0.3, 0.17], 0), (0.5, 0.2, 0), (0.88, 0, [0.1, 0.0, 0.05]),
+    (0.97, 0.0, 0.15), (1.0, 0, 0), (0.3, 0.7, 0),
+])
+@pytest.mark.parametrize("qn,kn", [(100, 1000), (20, 300), (7, 2500)])
+def test_block_mask_bit_exact(gpu, p, mn, mx, qn, kn):
+    from svoo_amd.co_clustering import block_mask_lengths
+
+    say("block_mask", p, mn, mx, qn, kn)
+    (qc, kc, qs, ks), (qct, kct, qst, kst) = _mask_case(gpu, 3, qn, kn, qn * kn)
+    m, lens = block_mask_lengths(qct, kct, qst, kst, p, mn, mx)
+    om, olens = O.identify_dynamic_map(qc, kc, qs, ks, p, mn, mx, return_lengths=True)
+    np.testing.assert_array_equal(m.cpu().numpy(), om)
+    np.testing.assert_array_equal(lens.cpu().numpy(), olens)
+
+
+def _attn_check(out, ref):
+    o = f32(out).astype(np.float64).reshape(-1)
+    r = np.asarray(ref, np.float64).reshape(-1)
+    err = np.abs(o - r).max()
+    cos = float(o @ r / (np.linalg.norm(o) * np.linalg.norm(r) + 1e-30))
+    assert err <= ATTN_MAX_ABS and cos >= ATTN_MIN_COS, (err, cos)
+    return err, cos
+
+
+@pytest.mark.parametrize("h,qn,kn,s,density,seed", [
+    (2, 12, 40, 3000, 0.3, 1), (1, 5, 9, 700, 0.6, 2), (3, 30, 200, 4096, 0.1, 3), (2, 4, 4, 333, 1.0, 4),
+])
+def test_vbsa_matches_oracle(gpu, h, qn, kn, s, density, seed):
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd
+
+    say("vbsa", h, qn, kn, s, density)
+    r = np.random.default_rng(seed)
+
+    def sizes(c):
+        cuts = np.sort(r.integers(0, s + 1, size=(h, c - 1)), axis=1)
+        z = np.concatenate([np.zeros((h, 1), int), cuts, np.full((h, 1), s)], axis=1)
+        return np.diff(z, axis=1).astype(np.int32)[None]
+
+    qs, ks = sizes(qn), sizes(kn)
+    m = r.random((1, h, qn, kn)) < density
+    m[0, 0, 0, :] = False  # an empty row
+    q, qt = rand_bf16((1, h, s, 128), seed, gpu)
+    k, kt = rand_bf16((1, h, s, 128), seed + 1, gpu)
+    v, vt = rand_bf16((1, h, s, 128), seed + 2, gpu)
+    out = dynamic_block_sparse_fwd(qt, kt, vt, torch.from_numpy(m).to(gpu), torch.from_numpy(qs).to(gpu),
+                                   torch.from_numpy(ks).to(gpu))
+    ref = O.block_sparse_attention(q, k, v, m, qs, ks)
+    _attn_check(out, ref)
+    a = int(qs[0, 0, 0])
+    assert torch.all(out[0, 0, :a] == 0)
+
+
+def test_vbsa_dense_equals_sdpa(gpu):
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd
+
+    say("vbsa dense vs sdpa")
+    h, s = 4, 2048
+    q, qt = rand_bf16((1, h, s, 128), 21, gpu)
+    k, kt = rand_bf16((1, h, s, 128), 22, gpu)
+    v, vt = rand_bf16((1, h, s, 128), 23, gpu)
+    qs = torch.full((1, h, 1), s, dtype=torch.int32, device=gpu)
+    m = torch.ones(1, h, 1, 1, dtype=torch.bool, device=gpu)
+    out = dynamic_block_sparse_fwd(qt, kt, vt, m, qs, qs)
+    ref = torch.nn.functional.scaled_dot_product_attention(qt.float(), kt.float(), vt.float())
+    _attn_check(out, ref.cpu().numpy())
+
+
+def test_vbsa_rejects_inconsistent_sizes(gpu):
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd_triton
+
+    say("vbsa bad sizes")
+    _, qt = rand_bf16((1, 1, 64, 128), 1, gpu)
+    qs = torch.tensor([[[30, 30]]], dtype=torch.int32, device=gpu)  # sums to 60 != 64
+    m = torch.ones(1, 1, 2, 2, dtype=torch.bool, device=gpu)
+    with pytest.raises(AssertionError):
+        dynamic_block_sparse_fwd_triton(qt, qt, qt, m, qs, qs)
+
+
+def test_vbsa_segments_expand_to_reference_plan(gpu):
+    from svoo_amd.co_clustering import vbsa_segments
+
+    say("vbsa segments")
+    r = np.random.default_rng(8)
+    bh, qn, kn = 3, 6, 50
+    m = r.random((bh, qn, kn)) < 0.3
+    cs = r.integers(0, 9, size=(bh, kn)).astype(np.int32)
+    start, length, count = vbsa_segments(torch.from_numpy(m).to(gpu), torch.from_numpy(cs).to(gpu))
+    start, length, count = start.cpu().numpy(), length.cpu().numpy(), count.cpu().numpy()
+    indptr, ind = O.kv_plan_indices(m, cs)
+    head_off = np.concatenate([[0], np.cumsum(cs.sum(1))[:-1]])
+    row = 0
+    for b in range(bh):
+        for i in range(qn):
+            toks = [np.arange(start[b, i, c], start[b, i, c] + length[b, i, c]) for c in range(count[b, i])]
+            toks = np.concatenate(toks) if toks else np.zeros(0, int)
+            np.testing.assert_array_equal(toks + head_off[b], ind[indptr[row]:indptr[row + 1]])
+            row += 1
+
+
+def test_golden_small_end_to_end(gpu):
+    """Co-clustering, mask and attention of the committed small case through the C ABI."""
+    from svoo_amd.co_clustering import block_mask_lengths, co_cluster_tokens_full, dynamic_block_sparse_fwd
+    from svoo_amd.permute import permute_pair_by_indices
+    from tests.golden.make_golden import MASK_CASES, SMALL, small_inputs
+    from pathlib import Path
+
+    say("golden small end to end")
+    g = np.load(Path(__file__).parent / "golden" / "golden_small.npz")
+    qb, kb, vb, qi, ki = small_inputs()
+    to_t = lambda b: torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).to(gpu)  # noqa: E731
+    q, k, v = to_t(qb), to_t(kb), to_t(vb)
+    r = co_cluster_tokens_full(q, k, SMALL.num_q_centroids, SMALL.num_k_centroids, SMALL.kmeans_iters,
+                               init_q_idx=torch.from_numpy(qi).to(gpu), init_k_idx=torch.from_numpy(ki).to(gpu))
+    ql, kl = r["qlabels"].cpu().numpy(), r["klabels"].cpu().numpy()
+    # well-separated synthetic mixture: the labels must match the oracle exactly
+    np.testing.assert_array_equal(ql, g["qlabels"])
+    np.testing.assert_array_equal(kl, g["klabels"])
+    np.testing.assert_array_equal(r["qcentroids"].view(torch.int16).cpu().numpy().view(np.uint16), g["qcent"])
+    np.testing.assert_array_equal(r["kcentroids"].view(torch.int16).cpu().numpy().view(np.uint16), g["kcent"])
+    np.testing.assert_array_equal(r["qsizes"].cpu().numpy(), g["qsizes"])
+    np.testing.assert_array_equal(r["k_sorted_idx"].cpu().numpy(), g["k_sorted_idx"])
+    h = SMALL.heads
+    for ci, (p, mn, mx) in enumerate(MASK_CASES):
+        m, lens = block_mask_lengths(r["qcentroids"][None], r["kcentroids"][None], r["qsizes"][None],
+                                     r["ksizes"][None], p, mn, mx)
+        np.testing.assert_array_equal(m[0].cpu().numpy(), g[f"map{ci}"])
+        np.testing.assert_array_equal(lens[0].cpu().numpy(), g[f"len{ci}"])
+    qp = torch.empty_like(q)
+    from svoo_amd import _lib
+
+    _lib.call("svoo_permute_rows", q.data_ptr(), r["q_sorted_idx"].data_ptr(), qp.data_ptr(), h, q.shape[1],
+              q.shape[1], 256, _lib.stream_of(gpu))
+    kp, vp = permute_pair_by_indices(k[None], v[None], r["k_sorted_idx"])
+    m0 = torch.from_numpy(g["map0"]).to(gpu)[None]
+    out = dynamic_block_sparse_fwd(qp[None], kp, vp, m0, r["qsizes"][None], r["ksizes"][None])
+    _attn_check(out[0], g["out_perm"].astype(np.float64))

@@ -1,0 +1,148 @@
+"""Host-side logic and the C ABI surface (CPU only, no kernel launches)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import svoo_oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def _header_symbols():
+    text = (ROOT / "include" / "svoo_hip.h").read_text()
+    return sorted(set(re.findall(r"\b(svoo_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from svoo_amd import _lib
+
+    syms = _header_symbols()
+    assert len(syms) >= 20
+    h = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [s for s in syms if not hasattr(h, s)]
+    assert not missing, missing
+    assert set(syms) == set(_lib.EXPORTED_SYMBOLS), set(syms) ^ set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_reports_errors_without_launching():
+    from svoo_amd import _lib
+
+    L = _lib.lib()
+    assert L.svoo_version() == 100
+    rc = L.svoo_vbsa_fwd(None, None, None, None, None, None, None, 1, 1, 128, 1, 1, None, 0, None, None)
+    assert rc == -1 and "null pointer" in _lib.last_error()
+    rc = L.svoo_block_mask(1, 1, 1, 1, 1, 1, 1, 1, 1, 64, 0.5, 0, 1, None, None)
+    assert rc == -2 and "D=64" in _lib.last_error()
+    assert L.svoo_co_cluster_workspace_size(40, 75600, 100, 1000, 128) > 0
+
+
+def test_product_code_never_touches_the_oracle():
+    for p in (ROOT / "svoo_amd").rglob("*.py"):
+        text = p.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle", text, re.M), p
+        assert "svoo_oracle" not in text, p
+
+
+@pytest.mark.parametrize("mn,mx", [
+    (0, 0), (0.2, 0), ([0.7, 0.15, 0.3], 0), ([0.2, 0.0, 0.05], [0.1, 0.3, 0.0]), (0.1, 0.05), (0, 0.001),
+    ([0.25, 0.25, 0.25], 0.1), (torch.tensor([0.1, 0.2, 0.3]), None), (np.array([0.3, 0.33, 0.7]), 0),
+])
+def test_mask_row_params_matches_oracle(mn, mx):
+    from svoo_amd.co_clustering import mask_row_params
+
+    for kn in (64, 500, 1000):
+        pre, cap = mask_row_params(3, kn, mn, mx)
+        opre, ocap = O.mask_row_params(3, kn, mn, mx)
+        assert pre == opre.tolist() and cap == ocap.tolist()
+
+
+def test_sparsity_lookup_fixture():
+    from svoo_amd.sparsity import SparsityLookup
+
+    lk = SparsityLookup(str(GOLDEN / "sparsity_wan_1.3B_t2v_steps1-3.csv"), verbose=False)
+    assert len(lk.lookup_dict) == 3 * 30 * 12
+    assert lk.get_sparsity(1, 0, 0) == pytest.approx(0.7382)
+    assert lk.get_sparsity(1, 0, 1) == pytest.approx(0.0411)
+    assert lk.get_sparsity(4, 0, 0) is None
+    assert lk.has_data_for_step_layer(2, 29, 12)
+    assert not lk.has_data_for_step_layer(4, 0, 12)
+    assert lk.get_sparsity_batch(9, 0, 3) == [0.0, 0.0, 0.0]
+    with pytest.raises(FileNotFoundError):
+        SparsityLookup(str(GOLDEN / "missing.csv"))
+
+
+def _proc(**kw):
+    from svoo_amd.processor import WanAttn_SAPAttn_Processor
+
+    cls = type("P", (WanAttn_SAPAttn_Processor,), dict(kw))
+    return cls(layer_idx=3)
+
+
+def test_reuse_schedule():
+    p = _proc(start_reuse_step=11, reuse_interval=40)
+    p._cached_clustering_results = {"x": 1}
+    got = []
+    for step in range(1, 51):
+        p.current_inference_step = step
+        got.append(p.should_recluster())
+    # Steps 1..10 always cluster, step 11 is the reuse anchor, 12..50 reuse (next recluster would be 51).
+    assert [s for s, r in zip(range(1, 51), got) if r] == list(range(1, 12))
+    p2 = _proc(start_reuse_step=11, reuse_interval=40)
+    p2.current_inference_step = 30
+    assert p2.should_recluster()  # nothing cached yet -> forced
+
+
+def test_dynamic_ratio_from_profile():
+    from svoo_amd.sparsity import SparsityLookup
+
+    lk = SparsityLookup(str(GOLDEN / "sparsity_wan_1.3B_t2v_steps1-3.csv"), verbose=False)
+    p = _proc(use_dynamic_min_kc_ratio=True, sparsity_lookup=lk, dynamic_min_kc_ratio_min=0.15,
+              dynamic_min_kc_ratio_max=0.20, min_kc_ratio=0.1)
+    vals = p._get_min_kc_ratio_for_heads_from_step(1, 12)
+    raw = lk.get_sparsity_batch(1, 3, 12)
+    assert vals == [min(max(v, 0.15), 0.20) for v in raw]
+    assert p._get_min_kc_ratio_for_heads_from_step(7, 12) == 0.1  # step missing -> scalar
+    assert p._get_min_kc_ratio_for_heads_from_step(None, 12) == 0.1
+
+
+def test_inference_step_counter():
+    p = _proc(_current_internal_timestep=None, _inference_step_counter=0, _seen_timesteps=set())
+    steps = [p._get_inference_step(t) for t in (999, 999, 980, 980, 950)]
+    assert steps == [1, 1, 2, 2, 3]
+    assert p._get_inference_step(999) == 1  # a larger timestep starts a new generation
+
+
+def test_synth_is_deterministic_and_head_separable():
+    from svoo_amd import synth
+
+    cfg = synth.SynthConfig("t", 5, 3, 2, 4, 4, 128, 8, 4, 6, 2, 0.1, 0.3, True, "bf16")
+    a = synth.make_qkv(cfg)
+    b = synth.make_qkv(cfg, heads=[2])
+    for x, y in zip(a, b):
+        assert torch.equal(x[:, 2:3], y)
+    c = synth.make_qkv(cfg)
+    assert all(torch.equal(x, y) for x, y in zip(a, c))
+    d = synth.head_densities(cfg)
+    assert all(0.1 <= r <= 0.3 for r in d) and d == synth.head_densities(cfg)
+
+
+def test_golden_fixture_matches_oracle():
+    from tests.golden.make_golden import MASK_CASES, SMALL, small_inputs
+
+    g = np.load(GOLDEN / "golden_small.npz")
+    qb, kb, vb, qi, ki = small_inputs()
+    np.testing.assert_array_equal(qi, g["q_init"])
+    q, k = O.bf16_from_bits(qb), O.bf16_from_bits(kb)
+    ql, qc, qs, kl, kc, ks = O.co_cluster_tokens(q, k, SMALL.num_q_centroids, SMALL.num_k_centroids,
+                                                 SMALL.kmeans_iters, init_q_idx=qi, init_k_idx=ki)
+    np.testing.assert_array_equal(ql, g["qlabels"])
+    np.testing.assert_array_equal(O.bf16_bits(kc), g["kcent"])
+    for ci, (p, mn, mx) in enumerate(MASK_CASES):
+        m = O.identify_dynamic_map(qc[None], kc[None], qs[None], ks[None], p, mn, mx)
+        np.testing.assert_array_equal(m[0], g[f"map{ci}"])

@@ -1,0 +1,265 @@
+"""Pins every oracle function with checks that do not restate it: library routines, closed forms,
+special cases, invariants and brute force on tiny inputs (CPU only).
+
+Pinning map (oracle function -> independent checks):
+  bf16_round / bf16_bits      torch's float32 -> bfloat16 conversion; hand-picked tie cases
+  cluster_sort                numpy stable argsort + bincount; edge cases (one cluster, K > N)
+  permute_rows / unpermute    fancy indexing; round trip; identity labels
+  centroid_update             exact rational means (fractions.Fraction); empty cluster keeps old
+  l2norm_rows                 numpy.linalg.norm
+  profile_centroids           unit rows; bf16-rounded matmul entries
+  cocluster_assign            brute force with math.fsum; reduced form argmax x.E; K == 1
+  co_cluster_tokens           well-separated mixture recovered exactly; fixed point of the update
+  weighted_softmax            scipy softmax (unit weights); closed form w / sum(w) for equal scores
+  identify_dynamic_map        p >= 1 all-true; p = 0 keeps max(1, int(r*Kc)); hand-computed top-p
+                              cut; prefix property; top-1 kept; float32 ratio semantics (0.7 -> 699)
+  kv_plan_indices             brute force on a hand-made map
+  block_sparse_attention      dense SDPA (torch, float64) for an all-true map; block-diagonal map;
+                              empty row -> 0
+  svoo_attention_call         one cluster + p >= 1 reduces to dense attention
+"""
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+from scipy.special import softmax as sp_softmax
+
+from oracle import svoo_oracle as O
+
+RNG = np.random.default_rng(1234)
+
+
+def test_bf16_round_matches_torch():
+    x = np.concatenate([
+        RNG.standard_normal(10000).astype(np.float32) * 10.0,
+        np.array([0.0, -0.0, 1.0, 1.00390625, 1.005859375, 3.4e38, -3.4e38, 1e-40, np.inf, -np.inf], np.float32),
+    ])
+    ours = O.bf16_round(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(ours, ref)
+    # ties to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> 1 (even mantissa)
+    assert O.bf16_round(np.float32(1.0 + 2 ** -8)) == np.float32(1.0)
+    assert O.bf16_round(np.float32(1.0 + 3 * 2 ** -8)) == np.float32(1.0 + 2 ** -6)
+    assert np.isnan(O.bf16_round(np.float32(np.nan)))
+
+
+@pytest.mark.parametrize("bh,n,k", [(3, 1000, 7), (2, 50, 64), (1, 1, 1), (2, 300, 1)])
+def test_cluster_sort_is_stable_counting_sort(bh, n, k):
+    labels = RNG.integers(0, k, size=(bh, n))
+    idx, sizes, offsets = O.cluster_sort(labels, k)
+    for r in range(bh):
+        np.testing.assert_array_equal(idx[r], np.argsort(labels[r], kind="stable"))
+        np.testing.assert_array_equal(sizes[r], np.bincount(labels[r], minlength=k))
+        np.testing.assert_array_equal(offsets[r], np.concatenate([[0], np.cumsum(sizes[r])[:-1]]))
+        assert np.all(np.diff(labels[r][idx[r]]) >= 0)
+
+
+def test_permute_unpermute_round_trip():
+    x = RNG.standard_normal((2, 97, 8)).astype(np.float32)
+    labels = RNG.integers(0, 5, size=(2, 97))
+    idx, _, _ = O.cluster_sort(labels, 5)
+    y = O.permute_rows(x, idx)
+    for r in range(2):
+        np.testing.assert_array_equal(y[r], x[r][idx[r]])
+    np.testing.assert_array_equal(O.unpermute_rows(y, idx), x)
+    ident = np.tile(np.arange(97), (2, 1))
+    idx2, _, _ = O.cluster_sort(ident, 97)
+    np.testing.assert_array_equal(O.permute_rows(x, idx2), x)
+
+
+def test_centroid_update_exact_means():
+    x = O.bf16_round(RNG.standard_normal((2, 60, 16)).astype(np.float32))
+    labels = RNG.integers(0, 6, size=(2, 60))
+    labels[1][labels[1] == 3] = 4  # cluster 3 of row 1 is empty
+    old = O.bf16_round(RNG.standard_normal((2, 6, 16)).astype(np.float32))
+    cent, cnt = O.centroid_update(x, labels, old)
+    for r in range(2):
+        for c in range(6):
+            members = x[r][labels[r] == c]
+            assert cnt[r, c] == len(members)
+            if len(members) == 0:
+                np.testing.assert_array_equal(cent[r, c], old[r, c])
+                continue
+            for d in range(16):
+                s = sum(Fraction(float(v)) for v in members[:, d])
+                s32 = np.float32(float(s))  # exact sum rounded once (these sums are exact in float64)
+                expect = O.bf16_round(np.float32(s32 / np.float32(len(members))))
+                assert cent[r, c, d] == expect
+
+
+def test_l2norm_rows():
+    x = RNG.standard_normal((5, 33))
+    np.testing.assert_allclose(O.l2norm_rows(x, 0.0), x / np.linalg.norm(x, axis=1, keepdims=True), rtol=1e-14)
+    z = np.zeros((1, 4))
+    np.testing.assert_array_equal(O.l2norm_rows(z), z)
+
+
+def test_profile_centroids_unit_rows_and_bf16_entries():
+    a = O.bf16_round(RNG.standard_normal((1, 9, 128)).astype(np.float32))
+    b = O.bf16_round(RNG.standard_normal((1, 5, 128)).astype(np.float32))
+    p = O.profile_centroids(a, b)
+    np.testing.assert_allclose(np.linalg.norm(p, axis=-1), 1.0, rtol=1e-9)
+    raw = torch.from_numpy(a).double() @ torch.from_numpy(b).double().transpose(-1, -2)
+    raw_bf = raw.float().to(torch.bfloat16).double().numpy()
+    np.testing.assert_allclose(p * np.linalg.norm(raw_bf, axis=-1, keepdims=True), raw_bf, rtol=1e-7, atol=1e-6)
+
+
+def test_cocluster_assign_brute_force_and_reduced_form():
+    x = O.bf16_round(RNG.standard_normal((1, 40, 128)).astype(np.float32))
+    c = O.bf16_round(RNG.standard_normal((1, 6, 128)).astype(np.float32))
+    cent = O.bf16_round(RNG.standard_normal((1, 9, 128)).astype(np.float32))
+    p = O.profile_centroids(cent, c)
+    labels, margin = O.cocluster_assign(x, c, p)
+    for n in range(40):
+        dots = [math.fsum(float(a) * float(b) for a, b in zip(x[0, n], c[0, kk])) for kk in range(6)]
+        norm = math.sqrt(math.fsum(d * d for d in dots) + 1e-8)
+        dist = [2.0 - 2.0 * math.fsum(dots[kk] / norm * p[0, j, kk] for kk in range(6)) for j in range(9)]
+        assert labels[0, n] == int(np.argmin(dist))
+        srt = sorted(dist)
+        assert margin[0, n] == pytest.approx(srt[1] - srt[0], abs=1e-12)
+    red = O.reduced_assign(x, c, p)
+    ok = margin > 1e-9
+    np.testing.assert_array_equal(red[ok], labels[ok])
+    one, _ = O.cocluster_assign(x, c, p[:, :1])
+    assert np.all(one == 0)
+
+
+def test_co_cluster_recovers_separated_mixture():
+    # Four far-apart components; queries and keys share the component -> exact recovery.
+    h, n, m = 1, 400, 4
+    mu = RNG.standard_normal((m, 128)) * 6.0
+    z = np.repeat(np.arange(m), n // m)
+    q = O.bf16_round((mu[z] + 0.05 * RNG.standard_normal((n, 128))).astype(np.float32))[None]
+    k = O.bf16_round((mu[z] + 0.05 * RNG.standard_normal((n, 128))).astype(np.float32))[None]
+    init = np.array([[0, 100, 200, 300]])
+    ql, qc, qs, kl, kc, ks = O.co_cluster_tokens(q, k, 4, 4, 3, init_q_idx=init, init_k_idx=init)
+    np.testing.assert_array_equal(ql[0], z)
+    np.testing.assert_array_equal(kl[0], z)
+    np.testing.assert_array_equal(qs[0], [100] * 4)
+    # Fixed point: centroids are the member means of the final labels.
+    again, _ = O.centroid_update(q, ql, qc)
+    np.testing.assert_array_equal(again, qc)
+    with pytest.raises(UnboundLocalError):
+        O.co_cluster_tokens(q, k, 4, 4, 0, init_q_idx=init, init_k_idx=init)
+
+
+def test_weighted_softmax_closed_forms():
+    s = O.bf16_round(RNG.standard_normal((3, 50)).astype(np.float32))
+    w = np.ones((3, 50))
+    np.testing.assert_array_equal(O.weighted_softmax(s, w), O.bf16_round(sp_softmax(s.astype(np.float64), axis=-1)))
+    eq = np.zeros((1, 7), np.float32)
+    wts = np.array([[1, 2, 3, 4, 0, 6, 7]], np.float64)
+    np.testing.assert_array_equal(O.weighted_softmax(eq, wts), O.bf16_round(wts / wts.sum()))
+    zero_w = O.weighted_softmax(eq, np.zeros((1, 7)))
+    np.testing.assert_array_equal(zero_w, np.zeros((1, 7), np.float32))
+
+
+def _centroids(h, qn, kn, seed=0):
+    r = np.random.default_rng(seed)
+    qc = O.bf16_round(r.standard_normal((1, h, qn, 128)).astype(np.float32))
+    kc = O.bf16_round(r.standard_normal((1, h, kn, 128)).astype(np.float32))
+    qs = r.integers(1, 50, size=(1, h, qn)).astype(np.int32)
+    ks = r.integers(0, 50, size=(1, h, kn)).astype(np.int32)
+    return qc, kc, qs, ks
+
+
+def test_mask_special_cases():
+    qc, kc, qs, ks = _centroids(2, 5, 40)
+    assert O.identify_dynamic_map(qc, kc, qs, ks, 1.0).all()
+    assert O.identify_dynamic_map(qc, kc, qs, ks, 0.5, min_kc_ratio=1.0).all()
+    m = O.identify_dynamic_map(qc, kc, qs, ks, 0.0, min_kc_ratio=[0.1, 0.35])
+    np.testing.assert_array_equal(m.sum(-1)[0, 0], [4] * 5)
+    # .item() of a float32 tensor gives float64(float32(0.35)) = 0.3499999940..., times 40 -> 13.99999976 -> 13
+    np.testing.assert_array_equal(m.sum(-1)[0, 1], [13] * 5)
+    m0 = O.identify_dynamic_map(qc, kc, qs, ks, 0.0)
+    np.testing.assert_array_equal(m0.sum(-1), np.ones((1, 2, 5)))
+
+
+def test_mask_keeps_top1_and_prefix():
+    qc, kc, qs, ks = _centroids(2, 6, 64, seed=3)
+    t = O.centroid_scores(qc, kc)
+    pb = O.weighted_softmax(t, np.broadcast_to(ks[:, :, None, :].astype(np.float64), t.shape))
+    for p in (0.3, 0.7, 0.9, 0.99):
+        m = O.identify_dynamic_map(qc, kc, qs, ks, p)
+        for h in range(2):
+            for i in range(6):
+                row = pb[0, h, i]
+                order = np.lexsort((np.arange(64), -row.astype(np.float64)))
+                kept = m[0, h, i][order]
+                nk = kept.sum()
+                assert kept[:nk].all() and not kept[nk:].any()  # a prefix of the stable order
+                assert kept[0]
+
+
+def test_mask_hand_computed_top_p():
+    # Equal centroid scores: p_j = w_j / sum(w) exactly; weights 8,4,2,1,1 (sum 16):
+    # probabilities 0.5, 0.25, 0.125, 0.0625, 0.0625 (all exact in bf16), prefix 0.5, 0.75, 0.875, 0.9375, 1.
+    qc = np.zeros((1, 1, 1, 128), np.float32)
+    kc = np.zeros((1, 1, 5, 128), np.float32)
+    ks = np.array([[[1, 2, 8, 4, 1]]], np.int32)  # sorted (stable) order: j=2,3,1,0,4
+    qs = np.ones((1, 1, 1), np.int32)
+    expect = {0.0: [2], 0.5: [2, 3], 0.74: [2, 3], 0.75: [2, 3, 1], 0.9: [2, 3, 1, 0], 0.99: [2, 3, 1, 0, 4]}
+    for p, keep in expect.items():
+        m = O.identify_dynamic_map(qc, kc, qs, ks, p)[0, 0, 0]
+        assert sorted(np.nonzero(m)[0].tolist()) == sorted(keep), p
+    # ties 0 and 4 (both 1/16): stable order keeps j=0 before j=4 at p = 0.9
+    m = O.identify_dynamic_map(qc, kc, qs, ks, 0.0, min_kc_ratio=0.8)[0, 0, 0]
+    assert np.nonzero(m)[0].tolist() == [0, 1, 2, 3]
+
+
+def test_mask_row_params_float32_ratio_semantics():
+    pre, cap = O.mask_row_params(2, 1000, [0.7, 0.15])
+    assert pre.tolist() == [699, 150]  # float32(0.7) * 1000 = 699.99998
+    pre, _ = O.mask_row_params(2, 1000, 0.7)
+    assert pre.tolist() == [700, 700]
+    pre, cap = O.mask_row_params(2, 1000, [0.2, 0.0], [0.1, 0.3])
+    assert cap.tolist() == [200, 300]
+    pre, cap = O.mask_row_params(2, 1000, 0.1, 0.05)
+    assert cap.tolist() == [100, 100]
+    pre, cap = O.mask_row_params(2, 100, 0, 0.001)
+    assert cap.tolist() == [1, 1]
+
+
+def test_kv_plan_indices_brute_force():
+    m = np.zeros((2, 2, 3), bool)
+    m[0, 0, [0, 2]] = True
+    m[1, 1, [1]] = True
+    cs = np.array([[2, 3, 1], [1, 1, 4]])
+    indptr, ind = O.kv_plan_indices(m, cs)
+    assert indptr.tolist() == [0, 3, 3, 3, 4]
+    assert ind.tolist() == [0, 1, 5, 7]
+
+
+def test_block_sparse_attention_closed_forms():
+    q = RNG.standard_normal((1, 2, 30, 128))
+    k = RNG.standard_normal((1, 2, 30, 128))
+    v = RNG.standard_normal((1, 2, 30, 128))
+    qs = np.array([[[10, 20], [15, 15]]])
+    ks = np.array([[[12, 18], [30, 0]]])
+    full = np.ones((1, 2, 2, 2), bool)
+    o = O.block_sparse_attention(q, k, v, full, qs, ks)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v)).numpy()
+    np.testing.assert_allclose(o, ref, rtol=1e-10, atol=1e-12)
+    diag = np.zeros((1, 2, 2, 2), bool)
+    diag[0, 0, 0, 0] = diag[0, 0, 1, 1] = True
+    diag[0, 1, 0, 0] = True  # head 1: cluster 1 has no active keys -> zeros
+    o = O.block_sparse_attention(q, k, v, diag, qs, ks)
+    blk = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q[:, :1, :10]), torch.from_numpy(k[:, :1, :12]), torch.from_numpy(v[:, :1, :12])).numpy()
+    np.testing.assert_allclose(o[:, :1, :10], blk, rtol=1e-10, atol=1e-12)
+    assert np.all(o[0, 1, 15:] == 0)
+
+
+def test_attention_call_reduces_to_dense():
+    h, n = 2, 64
+    q = O.bf16_round(RNG.standard_normal((1, h, n, 128)).astype(np.float32))
+    k = O.bf16_round(RNG.standard_normal((1, h, n, 128)).astype(np.float32))
+    v = O.bf16_round(RNG.standard_normal((1, h, n, 128)).astype(np.float32))
+    init = np.zeros((h, 1), np.int64)
+    out = O.svoo_attention_call(q, k, v, 1, 1, 2, 1.0, init_q_idx=init, init_k_idx=init)
+    dense = O.dense_attention(q, k, v)
+    np.testing.assert_allclose(out, np.transpose(dense, (0, 2, 1, 3)).reshape(1, n, h * 128), rtol=1e-9, atol=1e-12)
