@@ -1,0 +1,315 @@
+#!/usr/bin/env python3
+"""Benchmark of the SVOO attention call on one MI355X.
+
+One step is one full ``attention_core_logic`` call of the SVOO processor at the Wan2.1-14B 720p
+layer shape (H=40, N=75600, d=128, bf16): 5 warm-started co-clustering iterations (100 query /
+1000 key clusters), per-head block mask, permutes of Q/K/V, variable-block-sparse attention and
+the inverse permutation.  Inputs are synthetic (seeded Gaussian mixture with per-frame drift, drawn
+on the device) and resident in HBM before timing starts.
+
+Prints ONE JSON line: ``value`` is the dense-equivalent throughput ``4*H*N^2*d / t_call``
+(TFLOP/s), ``ms_per_step`` the call latency.  Extra fields give the stage breakdown (HIP events on
+the stream the kernels run on), the dense SDPA comparator at equal shape, the roofline of the
+dominant kernel (the sparse attention) and a CPU baseline (the numpy oracle on a bounded sample of
+the same inputs, rank 0 only).
+
+    python bench.py [--steps K] [--warmup W] [--config C3] [--mode density|reference]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "SVOO attention-call latency (ms) + effective TFLOP/s, Wan-14B 720p shape, 1 GPU"
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="C3", choices=["C2", "C3", "C4"])
+    ap.add_argument("--mode", default="density", choices=["density", "reference"],
+                    help="density: top_p=0, min_kc_ratio=rho_h; reference: top_p=0.9, min_kc_ratio=clip(rho_h,0.15,0.2)")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU baseline sample")
+    ap.add_argument("--traffic", default=str(ROOT / "profiles" / "vbsa_attn_C3_traffic.json"),
+                    help="measured HBM traffic of the attention kernel (from rocprofv3 --pmc), if present")
+    return ap.parse_args()
+
+
+def cpu_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        n = [i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"]
+        if n:
+            return int(max(n))
+    except Exception:
+        pass
+    return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the SVOO call is per-head independent and this build runs on "
+              "a single MI355X (multi-GPU sharding is design-only); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from svoo_amd import _lib, synth
+    from svoo_amd.co_clustering import co_cluster_tokens_full
+    from svoo_amd.processor import WanAttn_SAPAttn_Processor
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a HIP device")
+    _lib.lib()  # fail loudly if the HIP library is missing
+    dev = torch.device("cuda:0")
+    cfg = synth.CONFIGS[args.config]
+    h, n, d = cfg.heads, cfg.tokens, cfg.head_dim
+    qcn, kcn, iters = cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters
+    if cfg.text_tokens:
+        raise SystemExit("text-dense (HunyuanVideo) configs are not benchmarked by this script")
+
+    log(f"config {cfg.name}: H={h} N={n} d={d} Qc={qcn} Kc={kcn} iters={iters} mode={args.mode}")
+    t0 = time.time()
+    q, k, v = synth.make_qkv_device(cfg, dev)
+    torch.cuda.synchronize()
+    log(f"inputs drawn on device in {time.time() - t0:.1f}s")
+
+    rho = synth.head_densities(cfg)
+    if args.mode == "density":
+        top_p, ratios = 0.0, rho
+    else:
+        top_p, ratios = 0.9, [min(max(r, 0.15), 0.20) for r in rho]
+
+    # "Previous step": a clustering from seeded random token indices; the timed calls warm-start
+    # from its centroids perturbed by N(0, (0.05 rms)^2).
+    qi = synth.init_indices(cfg, h, qcn, n, 1).to(dev)
+    ki = synth.init_indices(cfg, h, kcn, n, 2).to(dev)
+    prev = co_cluster_tokens_full(q[0], k[0], qcn, kcn, iters, init_q_idx=qi, init_k_idx=ki)
+    q_init = synth.perturb_centroids(cfg, prev["qcentroids"], 3)
+    k_init = synth.perturb_centroids(cfg, prev["kcentroids"], 4)
+    del prev
+
+    class Proc(WanAttn_SAPAttn_Processor):
+        pass
+
+    Proc.num_frame, Proc.frame_size, Proc.context_length = cfg.frames, cfg.frame_size, 0
+    Proc.num_q_centroids, Proc.num_k_centroids = qcn, kcn
+    Proc.top_p_kmeans, Proc.min_kc_ratio, Proc.max_kc_ratio = top_p, ratios, 0
+    Proc.kmeans_iter_init = Proc.kmeans_iter_step = iters
+    Proc.kmeans_warm_start = True
+    Proc.centroids_init = True
+    Proc.enable_mem_save = True
+    proc = Proc(layer_idx=0)
+
+    def step(events=None):
+        proc.q_centroids, proc.k_centroids = q_init, k_init
+        proc._cached_clustering_results = None
+        proc.current_inference_step = None
+        proc.stage_events = events
+        return proc.attention_core_logic(q, k, v, timestep=None)
+
+    for _ in range(args.warmup):
+        out = step()
+    torch.cuda.synchronize()
+    log("warmup done")
+
+    # Timed region: K full calls; stage events are recorded on the current stream inside each call.
+    all_events = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        ev = []
+        out = step(ev)
+        all_events.append(ev)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    t_call_ms = start.elapsed_time(end) / args.steps
+    log(f"timed {args.steps} calls: {t_call_ms:.3f} ms/call (host wall {1e3 * wall / args.steps:.3f} ms/call)")
+
+    names = ["cluster", "permute", "mask", "attention", "unpermute"]
+    stage = {nm: [] for nm in names}
+    for ev in all_events:
+        marks = dict(ev)
+        prev_name = "start"
+        for nm in names:
+            stage[nm].append(marks[prev_name].elapsed_time(marks[nm]))
+            prev_name = nm
+    stages_ms = {nm: float(np.median(vals)) for nm, vals in stage.items()}
+    attn_ms_avg = float(np.mean(stage["attention"]))
+
+    # Work of the last call (every call starts from the same centroids, so all calls are equal).
+    last = proc._last_call
+    r = last["clustering"]
+    qs = r["qsizes"].to(torch.int64).view(1, h, qcn)
+    ks = r["ksizes"].to(torch.int64).view(1, h, kcn)
+    dmap = last["map"]
+    pairs = int((dmap.to(torch.int64) * qs[..., :, None] * ks[..., None, :]).sum().item())
+    active_flop = 4.0 * d * pairs
+    dense_flop = cfg.dense_flops()
+    realized_density = pairs / (h * float(n) ** 2)
+    active_tflops = active_flop / (attn_ms_avg * 1e-3) / 1e12
+    permute_bytes = 4 * (2 * h * n * d * 2 + h * n * 4)
+    permute_ms = stages_ms["permute"] + stages_ms["unpermute"]
+    eff_tflops = dense_flop / (t_call_ms * 1e-3) / 1e12
+
+    # Reuse step: clustering cached, mask + permutes + attention + unpermute only.
+    proc._step_from_callback = 2
+    Proc.start_reuse_step, Proc.reuse_interval = 1, 1000
+    proc.stage_events = None
+    proc.attention_core_logic(q, k, v, timestep=None)  # warm-up; reuses the last timed call's clustering
+    assert proc.should_recluster() is False
+    torch.cuda.synchronize()
+    rs, re_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    nreuse = max(3, args.steps // 2)
+    rs.record()
+    for _ in range(nreuse):
+        proc.attention_core_logic(q, k, v, timestep=None)
+    re_.record()
+    torch.cuda.synchronize()
+    reuse_ms = rs.elapsed_time(re_) / nreuse
+    del proc._step_from_callback
+    log(f"reuse step {reuse_ms:.3f} ms")
+
+    # Dense comparator: SDPA at equal shape (flash / memory-efficient kernels only).
+    t_sdpa_ms = None
+    if not args.no_dense:
+        try:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                o = torch.nn.functional.scaled_dot_product_attention(q, k, v)
+                torch.cuda.synchronize()
+                ds, de = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                reps = 2
+                ds.record()
+                for _ in range(reps):
+                    o = torch.nn.functional.scaled_dot_product_attention(q, k, v)
+                de.record()
+                torch.cuda.synchronize()
+                t_sdpa_ms = ds.elapsed_time(de) / reps
+                del o
+            log(f"dense SDPA {t_sdpa_ms:.2f} ms")
+        except Exception as e:  # the comparator is informative only
+            log(f"dense SDPA comparator unavailable: {e!r}")
+
+    traffic = None
+    tpath = Path(args.traffic)
+    if tpath.exists():
+        try:
+            tj = json.loads(tpath.read_text())
+            if tj.get("workload") == cfg.name and tj.get("mode") == args.mode:
+                traffic = float(tj["hbm_bytes_per_launch"])
+        except Exception as e:
+            log(f"traffic file unreadable: {e!r}")
+
+    roofline = {
+        "kernel": "vbsa_attn_kernel",
+        "bound": "mfma",
+        "achieved": round(active_tflops, 2),
+        "peak": BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(active_tflops / BF16_PEAK_TFLOPS, 4),
+        "traffic": traffic,
+        "avg_launch_ms": round(attn_ms_avg, 4),
+        "flop_per_launch": active_flop,
+    }
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, args.cpu_heads, t_call_ms)
+
+    line = {
+        "metric": METRIC,
+        "value": round(eff_tflops, 2),
+        "unit": "TFLOP/s (dense-equivalent, 4*H*N^2*d / t_call)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_call_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian mixture with per-frame drift, drawn on device)",
+        "config": {
+            "workload": f"{cfg.name}: one SVOO attention call, H={h} N={n} d={d} Qc={qcn} Kc={kcn}, "
+                        f"{iters} warm-started k-means iterations, {args.mode} mask mode",
+            "heads": h, "tokens": n, "head_dim": d, "q_clusters": qcn, "k_clusters": kcn,
+            "kmeans_iters": iters, "top_p": top_p, "mask_mode": args.mode,
+        },
+        "latency_ms": round(t_call_ms, 4),
+        "reuse_step_ms": round(reuse_ms, 4),
+        "stages_ms": {kk: round(vv, 4) for kk, vv in stages_ms.items()},
+        "realized_density": round(realized_density, 5),
+        "active_tflops": round(active_tflops, 2),
+        "permute_gbps": round(permute_bytes / (permute_ms * 1e-3) / 1e9, 1),
+        "permute_frac_hbm": round(permute_bytes / (permute_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "t_sdpa_ms": None if t_sdpa_ms is None else round(t_sdpa_ms, 3),
+        "speedup_vs_dense": None if t_sdpa_ms is None else round(t_sdpa_ms / t_call_ms, 3),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms):
+    """The numpy oracle on ``nheads`` heads of the same inputs; latency scaled linearly to all heads."""
+    import numpy as np
+
+    from oracle import svoo_oracle as O
+
+    h, n, d = cfg.heads, cfg.tokens, cfg.head_dim
+    sel = list(range(nheads))
+    f = lambda t: t[:, sel].float().cpu().numpy()  # noqa: E731
+    qn, kn, vn = f(q), f(k), f(v)
+    qi = q_init.view(h, -1, d)[sel].float().cpu().numpy()
+    ki = k_init.view(h, -1, d)[sel].float().cpu().numpy()
+    rs = [ratios[i] for i in sel]
+    t0 = time.perf_counter()
+    O.svoo_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
+                          init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
+    t = time.perf_counter() - t0
+    per_head = t / nheads
+    call_s = per_head * h
+    log(f"CPU oracle: {t:.2f}s for {nheads} head(s) -> {call_s:.1f}s per {h}-head call")
+    return {
+        "value": round(4.0 * nheads * float(n) ** 2 * d / t / 1e12, 5),
+        "unit": "TFLOP/s (dense-equivalent)",
+        "cores": cpu_threads(),
+        "kind": "port",
+        "sample": f"{nheads} of {h} heads of the same inputs, full call (k-means {cfg.kmeans_iters} warm-started "
+                  f"iterations, mask, permutes, fp32 block-sparse attention) in the numpy oracle: {t:.2f} s; "
+                  f"scaled x{h / nheads:g} to {call_s:.1f} s per call = {call_s * 1e3 / t_call_ms:.0f}x the GPU "
+                  f"latency",
+        "call_s_scaled": round(call_s, 3),
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -370,9 +370,9 @@ def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate
     out = torch.empty_like(qq)
     L = _lib.lib()
     ws = _lib.workspace(L.svoo_vbsa_workspace_size(bh, s, qn, kn), dev)
-    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev) if validate else None
     _lib.call("svoo_vbsa_fwd", qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), m.data_ptr(), qs.data_ptr(),
-              ks.data_ptr(), out.data_ptr(), bh, s, d, qn, kn, ws.data_ptr(), ws.numel(), status.data_ptr(),
+              ks.data_ptr(), out.data_ptr(), bh, s, d, qn, kn, ws.data_ptr(), ws.numel(), _lib.ptr(status),
               _lib.stream_of(dev))
     if validate and int(status.item()) != 0:
         raise AssertionError("cluster sizes of every head must sum to S (qc_size / kc_size)")

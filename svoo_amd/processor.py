@@ -104,6 +104,15 @@ class WanAttn_SAPAttn_Processor:
         self._cached_clustering_results = None
         self.current_inference_step = None
         self._last_call = None
+        # When set to a list, the sparse path appends (stage name, recorded torch.cuda.Event) at each
+        # stage boundary on the current stream: start, cluster, permute, mask, attention, unpermute.
+        self.stage_events = None
+
+    def _mark(self, name: str) -> None:
+        if self.stage_events is not None:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            self.stage_events.append((name, ev))
 
     # ---------------------------------------------------------------- diffusers glue
     def get_qkv(self, attn, hidden_states, encoder_hidden_states):
@@ -269,11 +278,13 @@ class WanAttn_SAPAttn_Processor:
         """
         cfg, num_heads, seq_len, dim = query.size()
         r = self.kmeans_clustering(query, key, self.layer_idx)
+        self._mark("cluster")
         min_kc_ratio = self._get_min_kc_ratio_for_heads_from_step(self.current_inference_step, num_heads)
         q_sizes = r["qsizes"].view(cfg, num_heads, self.num_q_centroids)
         k_sizes = r["ksizes"].view(cfg, num_heads, self.num_k_centroids)
         q_perm = _permute_rows(query, r["q_sorted_idx"])
         k_perm, v_perm = permute_pair_by_indices(key, value, r["k_sorted_idx"])
+        self._mark("permute")
         dynamic_map, lengths = block_mask_lengths(
             r["qcentroids"].view(cfg, num_heads, self.num_q_centroids, dim),
             r["kcentroids"].view(cfg, num_heads, self.num_k_centroids, dim),
@@ -312,9 +323,14 @@ class WanAttn_SAPAttn_Processor:
             out = self.flash_attention(query, key, value)
             return out.transpose(1, 2).flatten(2, 3)
 
+        self._mark("start")
         q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, q_sorted_indices = self.semantic_aware_permutation(
             query, key, value, timestep)
+        self._mark("mask")
         out_perm = dynamic_block_sparse_fwd(q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, validate=False)
+        self._mark("attention")
         if self.enable_mem_save:
             del q_perm, k_perm, v_perm
-        return apply_inverse_permutation_bshd(out_perm, q_sorted_indices)
+        out = apply_inverse_permutation_bshd(out_perm, q_sorted_indices)
+        self._mark("unpermute")
+        return out

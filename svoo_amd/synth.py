@@ -103,6 +103,33 @@ def make_qkv(cfg: SynthConfig, heads: Optional[Sequence[int]] = None, device="cp
     return tuple(qkv)
 
 
+def make_qkv_device(cfg: SynthConfig, device, seed_offset: int = 0):
+    """``(q, k, v)`` ``[1, H, N, d]`` in the config dtype, drawn on ``device`` with a seeded device generator.
+
+    Same mixture as :func:`make_head_qkv`, all heads at once (the full-size benchmark shapes take
+    seconds on the CPU).  The values differ from the CPU generator's; a CPU comparison copies
+    heads of these tensors back to the host.
+    """
+    dev = torch.device(device)
+    g = torch.Generator(device=dev)
+    g.manual_seed(cfg.seed * 1_000_003 + 7 + seed_offset)
+    h, n, d, m = cfg.heads, cfg.tokens, cfg.head_dim, cfg.mixture
+    dt = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
+    z = torch.randint(0, m, (h, n), generator=g, device=dev)
+    frame = (torch.arange(n, device=dev) // cfg.frame_size).to(torch.float32)[None, :, None]
+    out = []
+    for _ in range(3):
+        mu = torch.randn(h, m, d, generator=g, device=dev)
+        x = torch.gather(mu, 1, z[:, :, None].expand(h, n, d))
+        x.add_(torch.randn(h, n, d, generator=g, device=dev), alpha=0.3)
+        if cfg.drift:
+            delta = 0.02 * torch.randn(h, 1, d, generator=g, device=dev)
+            x.add_(frame * delta)
+        out.append(x.to(dt)[None].contiguous())
+        del x, mu
+    return tuple(out)
+
+
 def head_densities(cfg: SynthConfig, heads: Optional[Sequence[int]] = None) -> List[float]:
     """Per-head density ``rho_h ~ U[lo, hi]`` (seeded), used as the minimum key-cluster ratio."""
     g = torch.Generator(device="cpu")
