@@ -48,6 +48,25 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }
 
+// Two floats -> packed bf16 pair with the gfx950 conversion instruction (v_cvt_pk_bf16_f32,
+// round to nearest even); same values as pack_bf16x2 for every non-NaN input.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
+// gfx950 transposing LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes, lane i of the
+// group receives element e (e = 0..3) = element i%4 of the 8 bytes read by group lane 4e + i/4.
+// With group lane s addressing row (r0 + s/4), columns (c0 + 4*(s%4) .. +3) of a row-major bf16
+// matrix, lane i receives rows r0..r0+3 of column c0 + i.
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 ds_read_tr16_b64(const uint16_t* lds_ptr) {
+  const i16x4_t r =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(lds_ptr));
+  return __builtin_bit_cast(uint2, r);
+}
+
 // ---------------------------------------------------------------- block reductions
 template <int kThreads>
 __device__ __forceinline__ double block_sum_f64(double v, double* scratch) {

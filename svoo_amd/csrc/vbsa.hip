@@ -7,12 +7,12 @@
 //   * the block compacts its map row into a list of active key segments (start, length) in LDS;
 //     the KV stream is their concatenation (ascending cluster), cut into 64-key tiles that span
 //     segment boundaries, so padding happens once per work item instead of once per cluster;
-//   * per tile: K is staged row-major and V transposed (key-contiguous) in LDS; the next tile's
-//     rows are fetched into registers while the current tile computes;
+//   * per tile: K and V are staged row-major in LDS; the next tile's rows are fetched into
+//     registers while the current tile computes;
 //   * S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (keys on M, queries on N), so each lane holds 16
 //     keys of one query: the row max needs one cross-half exchange and the online-softmax rescale
-//     is a per-lane scalar;  O^T += V^T P^T reuses the S^T accumulators as the B operand directly
-//     (the V^T staging permutes keys to match the accumulator layout);
+//     is a per-lane scalar;  O^T += V^T P^T reuses the S^T accumulators as the B operand directly,
+//     with the V^T operand gathered by gfx950's transposing LDS read (ds_read_b64_tr_b16);
 //   * fp32 online softmax (exp2 with the scale folded in), P rounded to bf16 for the PV MFMA, as
 //     the reference's Triton kernel does; rows of a cluster with no active keys are written as 0.
 #include "svoo_common.h"
@@ -22,7 +22,7 @@ namespace svoo {
 constexpr int kVWaves = 4;
 constexpr int kKT = 64;          // keys per tile
 constexpr int kKStride = 136;    // bf16 per staged K row (128 + 8 pad)
-constexpr int kVStride = 72;     // bf16 per staged V^T row (64 keys + 8 pad)
+constexpr int kVStride = 160;    // bf16 per staged V row (128 + 32 pad: conflict-free transposed reads)
 constexpr int kPlanThreads = 256;
 constexpr int kMaxKN = 4096;
 
@@ -147,27 +147,35 @@ __device__ __forceinline__ int find_segment(const int32_t* seg_cum, int nseg, in
   return lo;
 }
 
-// Swap bits 2 and 3 of the tile key index: the V^T staging order that makes each lane's
-// eight PV operand keys contiguous (see the accumulator layout in svoo_common.h).
-__device__ __forceinline__ int vperm(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+// XCD-aware block -> work-item map: workgroups are dispatched round-robin over the 8 XCDs
+// (bid % 8), so runs of kXcdRun consecutive items (the q-tiles of one query cluster, which read
+// the same keys) are given to one XCD and start together, sharing that XCD's L2.
+constexpr int kXcdRun = 8;
+__device__ __forceinline__ long long xcd_item(long long bid) {
+  const long long x = bid % 8, j = bid / 8;
+  return (j / kXcdRun) * (8 * kXcdRun) + x * kXcdRun + (j % kXcdRun);
+}
 
 // ------------------------------------------------------------------------------------------ attention
+// Block = 4 waves x 32 queries of one query cluster.  Per 64-key tile:
+//   S^T = K Q^T   (A = K rows from LDS via ds_read_b128, B = Q held in registers), 16 MFMAs/wave;
+//   P = exp2(S * scale * log2e - m)  with a lazily updated running max m (rescale only when the
+//       tile max exceeds m by more than 8, i.e. P <= 2^8), P rounded to bf16 in registers;
+//   O^T += V^T P^T  (A = V columns read transposed from row-major LDS with ds_read_b64_tr_b16,
+//       B = the S^T accumulators' registers, whose key order the V read follows), 16 MFMAs/wave.
 template <int QB>
-__global__ void __launch_bounds__(kVWaves * kWave) vbsa_attn_kernel(
+__global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) vbsa_attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint8_t* __restrict__ map, const int32_t* __restrict__ ks, uint16_t* __restrict__ o, int s, int qn, int kn,
-    int cap, long long total_items, long long per_xcd, const int32_t* __restrict__ qoff,
-    const int32_t* __restrict__ koff, const int32_t* __restrict__ items, const int32_t* __restrict__ nitems,
-    float scale_log2) {
+    int cap, long long total_items, const int32_t* __restrict__ qoff, const int32_t* __restrict__ koff,
+    const int32_t* __restrict__ items, const int32_t* __restrict__ nitems, float scale_log2) {
   constexpr int kQTile = VbsaCfg<QB>::kQTile;
   __shared__ __attribute__((aligned(16))) uint16_t k_s[kKT * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_s[128 * kVStride];
+  __shared__ __attribute__((aligned(16))) uint16_t v_s[kKT * kVStride];
   __shared__ long long red[kVWaves];
   extern __shared__ int32_t seg_mem[];  // seg_start[kn], seg_cum[kn + 1]
 
-  // XCD-aware mapping: consecutive work items (same head, same q-cluster) share one XCD's L2.
-  const long long bid = blockIdx.x;
-  const long long item = (bid % 8) * per_xcd + bid / 8;
+  const long long item = xcd_item(blockIdx.x);
   if (item >= total_items) return;
   const int b = (int)(item / cap), local = (int)(item % cap);
   if (local >= nitems[b]) return;
@@ -178,6 +186,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) vbsa_attn_kernel(
   const int q1 = min(qo[ci + 1], q0 + kQTile);
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, h = lane / 32, l32 = lane % 32;
+  const int grp = lane / 16, gl = lane % 16;  // transposed-read group and lane within it
   const size_t head = (size_t)b * s * 128;
   const uint16_t* qb = q + head;
   const uint16_t* kb = k + head;
@@ -251,12 +260,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) vbsa_attn_kernel(
     for (int u = 0; u < 4; ++u) {
       const int r = rbase + 16 * u;
       *(u32x4_t*)(&k_s[r * kKStride + piece * 8]) = kreg[u];
-      const int pr = vperm(r);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vt_s[(piece * 8 + 2 * e) * kVStride + pr] = (uint16_t)(vreg[u][e] & 0xffffu);
-        vt_s[(piece * 8 + 2 * e + 1) * kVStride + pr] = (uint16_t)(vreg[u][e] >> 16);
-      }
+      *(u32x4_t*)(&v_s[r * kVStride + piece * 8]) = vreg[u];
     }
     __syncthreads();
     if (t + 1 < ntiles) fetch((t + 1) * kKT);
@@ -269,9 +273,9 @@ __global__ void __launch_bounds__(kVWaves * kWave) vbsa_attn_kernel(
       sacc[qbk][1] = f32x16_t{};
     }
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
+    for (int ks2 = 0; ks2 < 8; ++ks2) {
 #pragma unroll
-      for (int ks2 = 0; ks2 < 8; ++ks2) {
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
         const bf16x8_t a = as_bf16x8(*(const u32x4_t*)(&k_s[(kb2 * 32 + l32) * kKStride + ks2 * 16 + h * 8]));
 #pragma unroll
         for (int qbk = 0; qbk < QB; ++qbk) sacc[qbk][kb2] = mfma32x32x16(a, as_bf16x8(qop[qbk][ks2]), sacc[qbk][kb2]);
@@ -279,55 +283,69 @@ __global__ void __launch_bounds__(kVWaves * kWave) vbsa_attn_kernel(
     }
 
     // Online softmax (per lane: one query, 32 of the tile's 64 keys).
-    const int tbase = t * kKT;
+    const bool tail = (t + 1) * kKT > total;
     u32x4_t pop[QB][2][2];
 #pragma unroll
     for (int qbk = 0; qbk < QB; ++qbk) {
-      float mx = -INFINITY;
+      if (tail) {
+        const int tbase = t * kKT;
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+            if (tbase + key >= total) sacc[qbk][kb2][r] = -INFINITY;
+          }
+      }
+      float mx = sacc[qbk][0][0];
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
-          float sv = sacc[qbk][kb2][r] * scale_log2;
-          if (tbase + key >= total) sv = -INFINITY;
-          sacc[qbk][kb2][r] = sv;
-          mx = fmaxf(mx, sv);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[qbk], mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qbk] - m_new);
-      m_run[qbk] = m_new;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[qbk][kb2][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+      if (__any(mx > m_run[qbk] + 8.0f)) {
+        const float m_new = fmaxf(m_run[qbk], mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[qbk] - m_new);
+        m_run[qbk] = m_new;
+        l_run[qbk] *= alpha;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[qbk][db][r] *= alpha;
+      }
+      const float mneg = -m_run[qbk];
       float ls = 0.0f;
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2) {
         float pv[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          pv[r] = __builtin_amdgcn_exp2f(sacc[qbk][kb2][r] - m_new);
+          pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[qbk][kb2][r], scale_log2, mneg));
           ls += pv[r];
         }
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) pop[qbk][kb2][st][e] = pack_bf16x2(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
+          for (int e = 0; e < 4; ++e) pop[qbk][kb2][st][e] = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
       }
-      l_run[qbk] = l_run[qbk] * alpha + ls;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[qbk][db][r] *= alpha;
+      l_run[qbk] += ls;
     }
 
-    // O^T += V^T P^T.
+    // O^T += V^T P^T.  P^T operand element e of lane (query, h) is tile key 16st + 8(e/4) + 4h + e%4
+    // (the S^T accumulator layout); the V operand reads those keys' rows transposed: group grp
+    // gathers rows key0 + gl/4 (key0 = 32kb2 + 16st + 4(grp/2), +8 for elements 4..7), columns
+    // 32db + 16(grp%2) + 4(gl%4).
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2) {
+      for (int st = 0; st < 2; ++st) {
+        const int key0 = kb2 * 32 + st * 16 + 4 * (grp / 2) + gl / 4;
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const bf16x8_t a =
-              as_bf16x8(*(const u32x4_t*)(&vt_s[(db * 32 + l32) * kVStride + kb2 * 32 + st * 16 + h * 8]));
+        for (int db = 0; db < 4; ++db) {
+          const int col = db * 32 + 16 * (grp % 2) + 4 * (gl % 4);
+          const uint2 lo = ds_read_tr16_b64(&v_s[key0 * kVStride + col]);
+          const uint2 hi = ds_read_tr16_b64(&v_s[(key0 + 8) * kVStride + col]);
+          const bf16x8_t a = as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y});
 #pragma unroll
           for (int qbk = 0; qbk < QB; ++qbk) acc[qbk][db] = mfma32x32x16(a, as_bf16x8(pop[qbk][kb2][st]), acc[qbk][db]);
         }
@@ -349,8 +367,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) vbsa_attn_kernel(
         for (int g = 0; g < 4; ++g) {
           const int d0 = db * 32 + g * 8 + h * 4;
           uint2 w;
-          w.x = pack_bf16x2(acc[qbk][db][4 * g] * inv, acc[qbk][db][4 * g + 1] * inv);
-          w.y = pack_bf16x2(acc[qbk][db][4 * g + 2] * inv, acc[qbk][db][4 * g + 3] * inv);
+          w.x = cvt_pk_bf16(acc[qbk][db][4 * g] * inv, acc[qbk][db][4 * g + 1] * inv);
+          w.y = cvt_pk_bf16(acc[qbk][db][4 * g + 2] * inv, acc[qbk][db][4 * g + 3] * inv);
           *(uint2*)(dst + d0) = w;
         }
     }
@@ -441,12 +459,12 @@ extern "C" int svoo_vbsa_fwd(const uint16_t* q, const uint16_t* k, const uint16_
                      qoff, koff, items, nitems, status);
   if (int rc = check_launch("svoo_vbsa_fwd(plan)")) return rc;
   const long long total_items = (long long)bh * lay.cap;
-  const long long per_xcd = (total_items + 7) / 8;
+  const long long nblocks = (total_items + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
+  SVOO_REQUIRE(nblocks < (1ll << 31), SVOO_ERR_UNSUPPORTED, "svoo_vbsa_fwd: too many work items");
   const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)d));
   const size_t smem = (size_t)(2 * kn + 1) * sizeof(int32_t);
-  hipLaunchKernelGGL(vbsa_attn_kernel<kDefaultQB>, dim3((unsigned)(per_xcd * 8)), dim3(kVWaves * kWave), smem, st, q, k,
-                     v, map, k_sizes, o, s, qn, kn, lay.cap, total_items, per_xcd, qoff, koff, items, nitems,
-                     scale_log2);
+  hipLaunchKernelGGL(vbsa_attn_kernel<kDefaultQB>, dim3((unsigned)nblocks), dim3(kVWaves * kWave), smem, st, q, k, v,
+                     map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items, nitems, scale_log2);
   return check_launch("svoo_vbsa_fwd");
 }
 
