@@ -3,16 +3,17 @@
 // Plan (one block per batch-head, on device, no host round trip):
 //   qoff/koff = exclusive prefix of the cluster sizes (validated to sum to S), and a work list of
 //   (q-cluster, q-tile) items, kQTile queries each.
-// Attention (one block per work item, 4 waves, each wave owns 32*QB queries):
+// Attention (one block per work item, 4 waves, each wave owns 32*QB queries; 2 blocks per CU):
 //   * the block compacts its map row into a list of active key segments (start, length) in LDS;
 //     the KV stream is their concatenation (ascending cluster), cut into 64-key tiles that span
 //     segment boundaries, so padding happens once per work item instead of once per cluster;
-//   * per tile: K and V are staged row-major in LDS; the next tile's rows are fetched into
-//     registers while the current tile computes;
+//   * K and V tiles are double buffered in LDS and filled by LDS DMA (global_load_lds_dwordx4);
+//     wave 0 resolves the token rows of upcoming tiles into a small LDS table;
 //   * S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (keys on M, queries on N), so each lane holds 16
 //     keys of one query: the row max needs one cross-half exchange and the online-softmax rescale
 //     is a per-lane scalar;  O^T += V^T P^T reuses the S^T accumulators as the B operand directly,
 //     with the V^T operand gathered by gfx950's transposing LDS read (ds_read_b64_tr_b16);
+//   * the scores of tile t+1 are computed in the same iteration as the softmax of tile t;
 //   * fp32 online softmax (exp2 with the scale folded in), P rounded to bf16 for the PV MFMA, as
 //     the reference's Triton kernel does; rows of a cluster with no active keys are written as 0.
 #include "svoo_common.h"
@@ -21,8 +22,6 @@ namespace svoo {
 
 constexpr int kVWaves = 4;
 constexpr int kKT = 64;          // keys per tile
-constexpr int kKStride = 136;    // bf16 per staged K row (128 + 8 pad)
-constexpr int kVStride = 160;    // bf16 per staged V row (128 + 32 pad: conflict-free transposed reads)
 constexpr int kPlanThreads = 256;
 constexpr int kMaxKN = 4096;
 
@@ -157,12 +156,55 @@ __device__ __forceinline__ long long xcd_item(long long bid) {
 }
 
 // ------------------------------------------------------------------------------------------ attention
-// Block = 4 waves x 32 queries of one query cluster.  Per 64-key tile:
-//   S^T = K Q^T   (A = K rows from LDS via ds_read_b128, B = Q held in registers), 16 MFMAs/wave;
-//   P = exp2(S * scale * log2e - m)  with a lazily updated running max m (rescale only when the
-//       tile max exceeds m by more than 8, i.e. P <= 2^8), P rounded to bf16 in registers;
-//   O^T += V^T P^T  (A = V columns read transposed from row-major LDS with ds_read_b64_tr_b16,
-//       B = the S^T accumulators' registers, whose key order the V read follows), 16 MFMAs/wave.
+// Physical 16-byte chunk of logical chunk c in tile row r (rows are 256 bytes, unpadded).  The XOR
+// pattern makes both LDS read patterns conflict-free: 16 consecutive rows at one chunk (the K
+// operand reads) and 4 consecutive rows x 4 consecutive chunks (the transposed V reads).
+__device__ __forceinline__ int swz(int r, int c) { return c ^ (((r & 3) << 2) | ((r >> 2) & 3)); }
+
+// Position cursor over the segmented KV stream: row = off + p while p < next.
+struct KvCursor {
+  int seg, off, next;
+};
+__device__ __forceinline__ void cursor_init(KvCursor& c, const int32_t* seg_start, const int32_t* seg_cum, int nseg,
+                                            int p) {
+  c.seg = find_segment(seg_cum, nseg, p);
+  c.off = seg_start[c.seg] - seg_cum[c.seg];
+  c.next = seg_cum[c.seg + 1];
+}
+__device__ __forceinline__ int cursor_row(KvCursor& c, const int32_t* seg_start, const int32_t* seg_cum, int p) {
+  while (p >= c.next) {
+    ++c.seg;
+    c.off = seg_start[c.seg] - seg_cum[c.seg];
+    c.next = seg_cum[c.seg + 1];
+  }
+  return c.off + p;
+}
+
+// Block = kVWaves waves x 32 queries of one query cluster; K and V tiles of 64 keys are double
+// buffered in LDS with one barrier per tile.  Iteration t holds the scores S(t) in registers and
+//   * issues the global loads of K(t+2) and V(t+1) (registers), then
+//   * computes S(t+1) = K(t+1) Q^T (MFMA, A = K rows via ds_read_b128, B = Q in registers) next to
+//     the softmax of S(t) (VALU): P = exp2(S * scale * log2e - m) with a lazily updated running max
+//     m (rescale only when the tile max exceeds m by more than 8, i.e. P <= 2^8), bf16 P,
+//   * O^T += V(t)^T P^T (MFMA, A = V columns via the transposing LDS read, B = the score
+//     accumulators' registers, whose key order the V read follows),
+//   * stores K(t+2) and V(t+1) into the buffers freed by K(t) and V(t-1).
+// Direct global -> LDS copy of 16 bytes per lane: lane i writes lds_base + 16 i (gfx950 LDS DMA).
+__device__ __forceinline__ void lds_dma16(const void* src, uint16_t* lds_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
+// Block = kVWaves waves x 32 queries of one query cluster; K and V tiles of 64 keys are double
+// buffered in LDS, filled by LDS DMA, with one barrier per tile.  Iteration t holds the scores S(t)
+// in registers and
+//   * starts the DMA of K(t+2) and V(t+1) into the buffers freed by K(t) and V(t-1),
+//   * computes S(t+1) = K(t+1) Q^T (MFMA, A = K rows via ds_read_b128, B = Q in registers)
+//     interleaved with the softmax of S(t) (VALU): P = exp2(S * scale * log2e - m) with a lazily
+//     updated running max m (rescale only when the tile max exceeds m by more than 8, so P <= 2^8),
+//     bf16 P,
+//   * O^T += V(t)^T P^T (MFMA, A = V columns via the transposing LDS read, B = the score
+//     accumulators' registers, whose key order the V read follows).
 template <int QB>
 __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) vbsa_attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -170,9 +212,12 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     int cap, long long total_items, const int32_t* __restrict__ qoff, const int32_t* __restrict__ koff,
     const int32_t* __restrict__ items, const int32_t* __restrict__ nitems, float scale_log2) {
   constexpr int kQTile = VbsaCfg<QB>::kQTile;
-  __shared__ __attribute__((aligned(16))) uint16_t k_s[kKT * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t v_s[kKT * kVStride];
+  constexpr int kThreads = kVWaves * kWave;
+  constexpr int kDmaIt = kKT / (4 * kVWaves);  // 4-row DMA groups per wave per tile
+  __shared__ __attribute__((aligned(16))) uint16_t k_s0[kKT * 128], k_s1[kKT * 128];
+  __shared__ __attribute__((aligned(16))) uint16_t v_s0[kKT * 128], v_s1[kKT * 128];
   __shared__ long long red[kVWaves];
+  __shared__ int32_t rowtab[2][2][kKT];  // [K/V][slot][tile position] -> token row
   extern __shared__ int32_t seg_mem[];  // seg_start[kn], seg_cum[kn + 1]
 
   const long long item = xcd_item(blockIdx.x);
@@ -201,12 +246,14 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
 
   if (total == 0) {
     // Empty row: zero output (reference semantics, svoo/co_clustering.py:1102-1104).
-    for (int idx = tid; idx < (q1 - q0) * 16; idx += kVWaves * kWave) {
+    for (int idx = tid; idx < (q1 - q0) * 16; idx += kThreads) {
       const int r = idx / 16, c = idx % 16;
       ((u32x4_t*)(ob + (size_t)(q0 + r) * 128))[c] = u32x4_t{0u, 0u, 0u, 0u};
     }
     return;
   }
+  // Waves whose 32 queries all lie past the cluster still move K/V tiles but skip the math.
+  const bool active = q0 + wave * 32 * QB < q1;
 
   // Q operands (B of S^T = K Q^T): lane holds 8 consecutive d of its query per 16-wide k-step.
   u32x4_t qop[QB][8];
@@ -230,129 +277,175 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     l_run[qbk] = 0.0f;
   }
 
-  // Each thread moves 4 rows x 16 bytes of K and of V per tile: rows r_u = tid/16 + 16u, piece tid%16.
-  const int piece = tid % 16, rbase = tid / 16;
-  int cur[4];
+  // Row table: wave 0 resolves the 64 token rows of an upcoming K or V tile (lane = position) into
+  // rowtab one tile ahead of its use; positions past the stream map to the last valid row (finite
+  // values that the tail mask zeroes).
+  const int last_row = seg_start[nseg - 1] + (total - 1 - seg_cum[nseg - 1]);
+  KvCursor kcursor, vcursor;
+  if (wave == 0) {
+    cursor_init(kcursor, seg_start, seg_cum, nseg, min(lane, total - 1));
+    vcursor = kcursor;
+  }
+  auto resolve = [&](KvCursor& cur, int32_t* tab, int t) {
+    const int p = t * kKT + lane;
+    tab[lane] = p < total ? cursor_row(cur, seg_start, seg_cum, p) : last_row;
+  };
+  // DMA mapping: wave w, group j moves tile rows 4(kDmaIt w + j) + lane/16; lane writes physical
+  // chunk lane%16 of its row, i.e. fetches logical chunk swz(row, lane%16).
+  const int prow = lane / 16, pch = lane % 16;
+  auto dma = [&](const uint16_t* src, const int32_t* tab, uint16_t* buf) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) cur[u] = find_segment(seg_cum, nseg, min(rbase + 16 * u, total - 1));
-  u32x4_t kreg[4], vreg[4];
-  auto fetch = [&](int t0) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int p = t0 + rbase + 16 * u;
-      if (p < total) {
-        while (cur[u] + 1 < nseg && seg_cum[cur[u] + 1] <= p) ++cur[u];
-        const int row = seg_start[cur[u]] + (p - seg_cum[cur[u]]);
-        kreg[u] = ((const u32x4_t*)(kb + (size_t)row * 128))[piece];
-        vreg[u] = ((const u32x4_t*)(vb + (size_t)row * 128))[piece];
-      } else {
-        kreg[u] = u32x4_t{0u, 0u, 0u, 0u};
-        vreg[u] = u32x4_t{0u, 0u, 0u, 0u};
-      }
+    for (int j = 0; j < kDmaIt; ++j) {
+      const int r = 4 * (kDmaIt * wave + j) + prow;
+      lds_dma16(src + (size_t)tab[r] * 128 + swz(r, pch) * 8, buf + 4 * (kDmaIt * wave + j) * 128);
     }
   };
-
-  const int ntiles = (total + kKT - 1) / kKT;
-  fetch(0);
-  for (int t = 0; t < ntiles; ++t) {
-    __syncthreads();
+  // Lane offsets (bf16 elements) of the swizzled operand reads, loop invariant.
+  int koffs[8], voffs[2][4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int r = rbase + 16 * u;
-      *(u32x4_t*)(&k_s[r * kKStride + piece * 8]) = kreg[u];
-      *(u32x4_t*)(&v_s[r * kVStride + piece * 8]) = vreg[u];
+  for (int ks2 = 0; ks2 < 8; ++ks2) koffs[ks2] = l32 * 128 + swz(l32, ks2 * 2 + h) * 8;
+  {
+    const int r0 = 4 * (grp / 2) + gl / 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int c = 4 * db + 2 * (grp % 2) + (gl % 4) / 2, e0 = 4 * (gl % 2);
+      voffs[0][db] = r0 * 128 + swz(r0, c) * 8 + e0;
+      voffs[1][db] = (r0 + 8) * 128 + swz(r0 + 8, c) * 8 + e0;
     }
-    __syncthreads();
-    if (t + 1 < ntiles) fetch((t + 1) * kKT);
-
-    // S^T = K Q^T for the two 32-key blocks of the tile.
-    f32x16_t sacc[QB][2];
+  }
+  auto scores = [&](const uint16_t* kt, f32x16_t (&sa)[QB][2]) {
 #pragma unroll
     for (int qbk = 0; qbk < QB; ++qbk) {
-      sacc[qbk][0] = f32x16_t{};
-      sacc[qbk][1] = f32x16_t{};
+      sa[qbk][0] = f32x16_t{};
+      sa[qbk][1] = f32x16_t{};
     }
 #pragma unroll
     for (int ks2 = 0; ks2 < 8; ++ks2) {
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2) {
-        const bf16x8_t a = as_bf16x8(*(const u32x4_t*)(&k_s[(kb2 * 32 + l32) * kKStride + ks2 * 16 + h * 8]));
+        const bf16x8_t a = as_bf16x8(*(const u32x4_t*)(&kt[kb2 * 32 * 128 + koffs[ks2]]));
 #pragma unroll
-        for (int qbk = 0; qbk < QB; ++qbk) sacc[qbk][kb2] = mfma32x32x16(a, as_bf16x8(qop[qbk][ks2]), sacc[qbk][kb2]);
+        for (int qbk = 0; qbk < QB; ++qbk) sa[qbk][kb2] = mfma32x32x16(a, as_bf16x8(qop[qbk][ks2]), sa[qbk][kb2]);
       }
     }
+  };
 
-    // Online softmax (per lane: one query, 32 of the tile's 64 keys).
-    const bool tail = (t + 1) * kKT > total;
-    u32x4_t pop[QB][2][2];
-#pragma unroll
-    for (int qbk = 0; qbk < QB; ++qbk) {
-      if (tail) {
+  const int ntiles = (total + kKT - 1) / kKT;
+  f32x16_t sacc[QB][2], sacc2[QB][2];
+  // One tile: kcur holds K(t), knext K(t+1) (refilled with K(t+2)), vcur V(t), vnext (refilled with V(t+1)).
+  auto step = [&](int t, uint16_t* kbuf, const uint16_t* knext, const uint16_t* vbuf, uint16_t* vnext,
+                  f32x16_t (&sacc)[QB][2], f32x16_t (&snext)[QB][2]) {
+    if (t + 2 < ntiles) dma(kb, rowtab[0][t & 1], kbuf);
+    if (t + 1 < ntiles) dma(vb, rowtab[1][(t + 1) & 1], vnext);
+    if (wave == 0) {
+      if (t + 3 < ntiles) resolve(kcursor, rowtab[0][(t + 1) & 1], t + 3);
+      if (t + 2 < ntiles) resolve(vcursor, rowtab[1][t & 1], t + 2);
+    }
+    if (active) {
+      if ((t + 1) * kKT > total) {
         const int tbase = t * kKT;
+#pragma unroll
+        for (int qbk = 0; qbk < QB; ++qbk)
+#pragma unroll
+          for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+              if (tbase + key >= total) sacc[qbk][kb2][r] = -INFINITY;
+            }
+      }
+#pragma unroll
+      for (int qbk = 0; qbk < QB; ++qbk) {
+        float mx = sacc[qbk][0][0];
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[qbk][kb2][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+        if (__any(mx > m_run[qbk] + 8.0f)) {
+          const float m_new = fmaxf(m_run[qbk], mx);
+          const float alpha = __builtin_amdgcn_exp2f(m_run[qbk] - m_new);
+          m_run[qbk] = m_new;
+          l_run[qbk] *= alpha;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[qbk][db][r] *= alpha;
+        }
+      }
+      // One scheduling region: S(t+1) MFMAs (computed on stale data and discarded after the last
+      // tile) interleaved with the exponentials of S(t), then PV(t).
+      scores(knext, snext);
+      u32x4_t pop[QB][2][2];
+#pragma unroll
+      for (int qbk = 0; qbk < QB; ++qbk) {
+        const float mneg = -m_run[qbk];
+        float ls = 0.0f;
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) {
+          float pv[16];
+#pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int key = kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
-            if (tbase + key >= total) sacc[qbk][kb2][r] = -INFINITY;
+            pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[qbk][kb2][r], scale_log2, mneg));
+            ls += pv[r];
           }
+#pragma unroll
+          for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pop[qbk][kb2][st][e] = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
+        }
+        l_run[qbk] += ls;
       }
-      float mx = sacc[qbk][0][0];
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[qbk][kb2][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
-      if (__any(mx > m_run[qbk] + 8.0f)) {
-        const float m_new = fmaxf(m_run[qbk], mx);
-        const float alpha = __builtin_amdgcn_exp2f(m_run[qbk] - m_new);
-        m_run[qbk] = m_new;
-        l_run[qbk] *= alpha;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[qbk][db][r] *= alpha;
-      }
-      const float mneg = -m_run[qbk];
-      float ls = 0.0f;
+      // O^T += V(t)^T P^T.  Element e of lane (query, h) of the P^T operand is tile key
+      // 16st + 8(e/4) + 4h + e%4 (the score accumulator layout); group grp of the transposed read
+      // gathers rows key0 + gl/4 (key0 = 32kb2 + 16st + 4(grp/2), +8 for elements 4..7) at columns
+      // 32db + 16(grp%2) + 4(gl%4).
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2) {
-        float pv[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[qbk][kb2][r], scale_log2, mneg));
-          ls += pv[r];
+        for (int st = 0; st < 2; ++st) {
+          const int rb = (kb2 * 32 + st * 16) * 128;
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            const uint2 lo = ds_read_tr16_b64(&vbuf[rb + voffs[0][db]]);
+            const uint2 hi = ds_read_tr16_b64(&vbuf[rb + voffs[1][db]]);
+            const bf16x8_t a = as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+            for (int qbk = 0; qbk < QB; ++qbk)
+              acc[qbk][db] = mfma32x32x16(a, as_bf16x8(pop[qbk][kb2][st]), acc[qbk][db]);
+          }
         }
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) pop[qbk][kb2][st][e] = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
       }
-      l_run[qbk] += ls;
     }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS DMA has landed
+    __syncthreads();
+  };
 
-    // O^T += V^T P^T.  P^T operand element e of lane (query, h) is tile key 16st + 8(e/4) + 4h + e%4
-    // (the S^T accumulator layout); the V operand reads those keys' rows transposed: group grp
-    // gathers rows key0 + gl/4 (key0 = 32kb2 + 16st + 4(grp/2), +8 for elements 4..7), columns
-    // 32db + 16(grp%2) + 4(gl%4).
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const int key0 = kb2 * 32 + st * 16 + 4 * (grp / 2) + gl / 4;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          const int col = db * 32 + 16 * (grp % 2) + 4 * (gl % 4);
-          const uint2 lo = ds_read_tr16_b64(&v_s[key0 * kVStride + col]);
-          const uint2 hi = ds_read_tr16_b64(&v_s[(key0 + 8) * kVStride + col]);
-          const bf16x8_t a = as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y});
-#pragma unroll
-          for (int qbk = 0; qbk < QB; ++qbk) acc[qbk][db] = mfma32x32x16(a, as_bf16x8(pop[qbk][kb2][st]), acc[qbk][db]);
-        }
-      }
-    }
+  // Prologue: row tables of K(0), K(1), V(0); DMA K(0), V(0) -> buffers 0 and K(1) -> K buffer 1;
+  // S(0) while wave 0 resolves K(2) and V(1).
+  if (wave == 0) {
+    resolve(kcursor, rowtab[0][0], 0);
+    if (ntiles > 1) resolve(kcursor, rowtab[0][1], 1);
+    resolve(vcursor, rowtab[1][0], 0);
+  }
+  __syncthreads();
+  dma(kb, rowtab[0][0], k_s0);
+  dma(vb, rowtab[1][0], v_s0);
+  if (ntiles > 1) dma(kb, rowtab[0][1], k_s1);
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (active) scores(k_s0, sacc);
+  if (wave == 0) {
+    if (ntiles > 2) resolve(kcursor, rowtab[0][0], 2);
+    if (ntiles > 1) resolve(vcursor, rowtab[1][1], 1);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, k_s0, k_s1, v_s0, v_s1, sacc, sacc2);
+    if (t + 1 < ntiles) step(t + 1, k_s1, k_s0, v_s1, v_s0, sacc2, sacc);
   }
 
+  if (!active) return;
   // Normalise and store: lane holds d = db*32 + (r/4)*8 + 4h + r%4 of query l32.
 #pragma unroll
   for (int qbk = 0; qbk < QB; ++qbk) {
