@@ -11,7 +11,7 @@
 
 namespace svoo {
 
-constexpr int kCentPosPerWave = 256;
+constexpr int kCentPosPerWave = 128;
 constexpr int kCentUnroll = 8;
 
 __global__ void __launch_bounds__(256) centroid_accumulate_kernel(const uint32_t* __restrict__ x,

@@ -19,7 +19,8 @@ constexpr int kAssignChunk = 64;   // E rows staged in LDS per step
 constexpr int kLdsRow = 136;       // bf16 elements per staged row (128 + 8 pad)
 
 // --------------------------------------------------------------------------------------- prep
-// kPrepRows rows of A per block (8 for profile widths up to 1664, else 2, to fit 64 KB of LDS).
+// kPrepRows rows of A per block: 8 when there are many rows (the key side) and the profile width
+// is at most 1664 (LDS), else 2 (more blocks for the few, long query-side rows).
 template <int kPrepRows>
 __global__ void __launch_bounds__(256) cocluster_prep_kernel(const uint16_t* __restrict__ a,
                                                              const uint16_t* __restrict__ bmat,
@@ -223,7 +224,8 @@ static size_t prep_smem(int rows, int kp) {
 
 static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uint16_t* e_lo, float* profile, int bh,
                        int j, int kp, int jpad, hipStream_t stream) {
-  if ((size_t)8 * kp * sizeof(float) <= (size_t)kPrepMaxLds) {
+  // Few rows (the query side) -> 2 rows per block for more blocks; many rows -> 8 rows per block.
+  if (j >= 512 && (size_t)8 * kp * sizeof(float) <= (size_t)kPrepMaxLds) {
     hipLaunchKernelGGL(cocluster_prep_kernel<8>, dim3(jpad / 8, bh), dim3(256), prep_smem(8, kp), stream, a, b, e_hi,
                        e_lo, profile, j, kp, jpad);
   } else {

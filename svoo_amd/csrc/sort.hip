@@ -3,9 +3,11 @@
 // Three HBM-light passes over labels[BH][N] (int32):
 //   1. hist:    per 1024-token chunk, an LDS histogram -> counts[b][k][chunk]   (cluster-major)
 //   2. scan:    per row, exclusive scan of counts in (cluster, chunk) order      -> chunk bases,
-//               sizes[b][k] and offsets[b][k]
-//   3. scatter: one wave per chunk walks its tokens in order, 64 at a time; lanes with the same
-//               label are ranked by lane order (ballot + popcount), so equal labels keep their
+//               sizes[b][k] and offsets[b][k]; 16 waves each scan a contiguous span 64 entries
+//               at a time (coalesced), after a first pass that sums each span
+//   3. scatter: one wave per chunk walks its tokens in order, 64 at a time; the lanes holding the
+//               same label are found with one ballot per label bit (ceil(log2 K) ballots), and
+//               ranked by lane order (popcount of the lower lanes), so equal labels keep their
 //               original token order (stable).
 #include "svoo_common.h"
 
@@ -37,34 +39,61 @@ __global__ void __launch_bounds__(256) sort_hist_kernel(const int32_t* __restric
   for (int i = threadIdx.x; i < k; i += blockDim.x) out[(size_t)i * nchunks + c] = hist[i];
 }
 
-__global__ void __launch_bounds__(1024) sort_scan_kernel(int32_t* __restrict__ counts, int k, int nchunks,
-                                                         int32_t* __restrict__ sizes, int32_t* __restrict__ offsets) {
-  __shared__ long long scratch[1024 / kWave];
-  const int b = blockIdx.x;
+constexpr int kScanWaves = 16;
+
+__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int n = __shfl_up(v, o);
+    if (lane >= o) v += n;
+  }
+  return v;
+}
+
+__global__ void __launch_bounds__(kScanWaves * kWave) sort_scan_kernel(int32_t* __restrict__ counts, int k,
+                                                                       int nchunks, int32_t* __restrict__ sizes,
+                                                                       int32_t* __restrict__ offsets) {
+  __shared__ int wsum[kScanWaves];
+  __shared__ int wbase[kScanWaves + 1];
+  const int b = blockIdx.x, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   int32_t* cnt = counts + (size_t)b * k * nchunks;
-  const long long total = (long long)k * nchunks;
-  const long long per = (total + blockDim.x - 1) / blockDim.x;
-  const long long s = min(total, per * threadIdx.x), e = min(total, s + per);
-  long long local = 0;
-  for (long long i = s; i < e; ++i) local += cnt[i];
-  long long all;
-  long long run = block_exclusive_scan_i64<1024>(local, scratch, &all);
-  for (long long i = s; i < e; ++i) {
-    const int32_t v = cnt[i];
-    cnt[i] = (int32_t)run;
-    run += v;
+  const int total = k * nchunks;
+  const int per = ((total + kScanWaves - 1) / kScanWaves + kWave - 1) / kWave * kWave;
+  const int s0 = min(total, wave * per), s1 = min(total, s0 + per);
+  int acc = 0;
+  for (int i = s0 + lane; i < s1; i += kWave) acc += cnt[i];
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) wsum[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int r = 0;
+    for (int w = 0; w < kScanWaves; ++w) {
+      wbase[w] = r;
+      r += wsum[w];
+    }
+    wbase[kScanWaves] = r;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < k; i += blockDim.x) {
+  int run = wbase[wave];
+  for (int g = s0; g < s1; g += kWave) {
+    const int i = g + lane;
+    const int v = i < s1 ? cnt[i] : 0;
+    const int inc = wave_inclusive_scan(v, lane);
+    if (i < s1) cnt[i] = run + inc - v;
+    run += __shfl(inc, kWave - 1);
+  }
+  __syncthreads();
+  const int all = wbase[kScanWaves];
+  for (int i = threadIdx.x; i < k; i += kScanWaves * kWave) {
     const int32_t start = cnt[(size_t)i * nchunks];
-    const int32_t next = (i + 1 < k) ? cnt[(size_t)(i + 1) * nchunks] : (int32_t)all;
+    const int32_t next = (i + 1 < k) ? cnt[(size_t)(i + 1) * nchunks] : all;
     offsets[(size_t)b * k + i] = start;
     sizes[(size_t)b * k + i] = next - start;
   }
 }
 
 __global__ void __launch_bounds__(64) sort_scatter_kernel(const int32_t* __restrict__ labels, int n, int k,
-                                                          int nchunks, const int32_t* __restrict__ bases,
+                                                          int kbits, int nchunks, const int32_t* __restrict__ bases,
                                                           int32_t* __restrict__ sorted_idx,
                                                           int32_t* __restrict__ sorted_labels) {
   extern __shared__ int32_t base[];
@@ -79,27 +108,27 @@ __global__ void __launch_bounds__(64) sort_scatter_kernel(const int32_t* __restr
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int t0 = s; t0 < e; t0 += kWave) {
     const int t = t0 + lane;
-    const bool valid = t < e;
-    int l = valid ? lab[t] : -1;
+    int l = t < e ? lab[t] : -1;
     if ((unsigned)l >= (unsigned)k) l = -1;  // out-of-range labels were flagged by the hist pass
-    unsigned long long pending = __ballot(l >= 0);
-    while (pending) {
-      const int leader = __ffsll((long long)pending) - 1;
-      const int ll = __shfl(l, leader);
-      const unsigned long long same = __ballot(l == ll) & pending;
-      const int bval = base[ll];
-      if (l == ll) {
-        const int pos = bval + __popcll(same & below);
-        if ((unsigned)pos < (unsigned)n) {  // always true for consistent bases; guards memory anyway
-          out[pos] = t;
-          if (outl) outl[pos] = ll;
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
-      if (lane == leader) base[ll] = bval + __popcll(same);
-      __builtin_amdgcn_wave_barrier();
-      pending &= ~same;
+    // Lanes with the same label: one ballot per label bit.
+    unsigned long long same = __ballot(l >= 0);
+    for (int bit = 0; bit < kbits; ++bit) {
+      const bool on = (l >> bit) & 1;
+      const unsigned long long bal = __ballot(on);
+      same &= on ? bal : ~bal;
     }
+    if (l >= 0) {
+      const int rank = __popcll(same & below);
+      const int cnt = __popcll(same);
+      const int bval = base[l];
+      const int pos = bval + rank;
+      if ((unsigned)pos < (unsigned)n) {  // always true for consistent bases; guards memory anyway
+        out[pos] = t;
+        if (outl) outl[pos] = l;
+      }
+      if (rank == cnt - 1) base[l] = bval + cnt;
+    }
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -119,11 +148,15 @@ int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t*
                            int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
                            hipStream_t stream) {
   const int nch = sort_nchunks(n);
+  SVOO_REQUIRE((long long)k * nch < (1ll << 31), SVOO_ERR_UNSUPPORTED, "svoo_cluster_sort: k=%d x %d chunks too large",
+               k, nch);
   hipLaunchKernelGGL(sort_hist_kernel, dim3(nch, bh), dim3(256), k * sizeof(int32_t), stream, labels, n, k, nch,
                      counts, err);
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(bh), dim3(1024), 0, stream, counts, k, nch, sizes, offsets);
-  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nch, bh), dim3(64), k * sizeof(int32_t), stream, labels, n, k, nch,
-                     counts, sorted_idx, sorted_labels);
+  int kbits = 0;
+  while ((1 << kbits) < k) ++kbits;
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(bh), dim3(kScanWaves * kWave), 0, stream, counts, k, nch, sizes, offsets);
+  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nch, bh), dim3(64), k * sizeof(int32_t), stream, labels, n, k, kbits,
+                     nch, counts, sorted_idx, sorted_labels);
   return check_launch("svoo_cluster_sort");
 }
 
