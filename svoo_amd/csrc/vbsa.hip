@@ -3,24 +3,26 @@
 // Plan (one block per batch-head, on device, no host round trip):
 //   qoff/koff = exclusive prefix of the cluster sizes (validated to sum to S), and a work list of
 //   (q-cluster, q-tile) items, kQTile queries each.
-// Attention (one block per work item, 4 waves, each wave owns 32*QB queries; 2 blocks per CU):
+// Attention (one block of 8 waves per work item of 256 queries, 32 queries per wave):
 //   * the block compacts its map row into a list of active key segments (start, length) in LDS;
 //     the KV stream is their concatenation (ascending cluster), cut into 64-key tiles that span
 //     segment boundaries, so padding happens once per work item instead of once per cluster;
 //   * K and V tiles are double buffered in LDS and filled by LDS DMA (global_load_lds_dwordx4);
-//     wave 0 resolves the token rows of upcoming tiles into a small LDS table;
+//     two waves resolve the token rows of upcoming tiles into a small LDS table;
 //   * S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (keys on M, queries on N), so each lane holds 16
 //     keys of one query: the row max needs one cross-half exchange and the online-softmax rescale
 //     is a per-lane scalar;  O^T += V^T P^T reuses the S^T accumulators as the B operand directly,
 //     with the V^T operand gathered by gfx950's transposing LDS read (ds_read_b64_tr_b16);
-//   * the scores of tile t+1 are computed in the same iteration as the softmax of tile t;
+//   * ping-pong: the two waves sharing a SIMD belong to two groups that alternate, one half-step
+//     apart, between the MFMA work of a tile and the softmax of the next, so matrix and vector
+//     units are busy at the same time;
 //   * fp32 online softmax (exp2 with the scale folded in), P rounded to bf16 for the PV MFMA, as
 //     the reference's Triton kernel does; rows of a cluster with no active keys are written as 0.
 #include "svoo_common.h"
 
 namespace svoo {
 
-constexpr int kVWaves = 4;
+constexpr int kVWaves = 8;
 constexpr int kKT = 64;          // keys per tile
 constexpr int kPlanThreads = 256;
 constexpr int kMaxKN = 4096;
@@ -195,16 +197,12 @@ __device__ __forceinline__ void lds_dma16(const void* src, uint16_t* lds_base) {
                                    (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
-// Block = kVWaves waves x 32 queries of one query cluster; K and V tiles of 64 keys are double
-// buffered in LDS, filled by LDS DMA, with one barrier per tile.  Iteration t holds the scores S(t)
-// in registers and
-//   * starts the DMA of K(t+2) and V(t+1) into the buffers freed by K(t) and V(t-1),
-//   * computes S(t+1) = K(t+1) Q^T (MFMA, A = K rows via ds_read_b128, B = Q in registers)
-//     interleaved with the softmax of S(t) (VALU): P = exp2(S * scale * log2e - m) with a lazily
-//     updated running max m (rescale only when the tile max exceeds m by more than 8, so P <= 2^8),
-//     bf16 P,
-//   * O^T += V(t)^T P^T (MFMA, A = V columns via the transposing LDS read, B = the score
-//     accumulators' registers, whose key order the V read follows).
+// Ping-pong block: 8 waves in two groups of 4 (group A = waves 0-3, group B = waves 4-7), each
+// wave 32 queries (query tile 256: A owns queries 0-127, B 128-255).  The waves of a SIMD come
+// from different groups and alternate between an MFMA phase M(t) = {O += V(t)^T P(t)^T, S(t+1) =
+// K(t+1) Q^T} and a VALU phase V(t) = {softmax of S(t) -> P(t)}; group B runs one half-step behind
+// group A, so in every half-step one wave per SIMD does MFMA work while the other does VALU work.
+// Group B also issues the LDS DMA of the next K/V tiles and resolves their token rows.
 template <int QB>
 __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) vbsa_attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -213,7 +211,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     const int32_t* __restrict__ items, const int32_t* __restrict__ nitems, float scale_log2) {
   constexpr int kQTile = VbsaCfg<QB>::kQTile;
   constexpr int kThreads = kVWaves * kWave;
-  constexpr int kDmaIt = kKT / (4 * kVWaves);  // 4-row DMA groups per wave per tile
+  constexpr int kDmaIt = kKT / (4 * 4);  // 4-row DMA groups per group-B wave per tile and matrix
   __shared__ __attribute__((aligned(16))) uint16_t k_s0[kKT * 128], k_s1[kKT * 128];
   __shared__ __attribute__((aligned(16))) uint16_t v_s0[kKT * 128], v_s1[kKT * 128];
   __shared__ long long red[kVWaves];
@@ -232,6 +230,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, h = lane / 32, l32 = lane % 32;
   const int grp = lane / 16, gl = lane % 16;  // transposed-read group and lane within it
+  const bool group_b = wave >= 4;
+  const int wg = wave & 3;
   const size_t head = (size_t)b * s * 128;
   const uint16_t* qb = q + head;
   const uint16_t* kb = k + head;
@@ -252,55 +252,39 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     }
     return;
   }
-  // Waves whose 32 queries all lie past the cluster still move K/V tiles but skip the math.
-  const bool active = q0 + wave * 32 * QB < q1;
+  const int qrow0 = q0 + (group_b ? 128 : 0) + wg * 32;
+  const bool active = qrow0 < q1;
 
-  // Q operands (B of S^T = K Q^T): lane holds 8 consecutive d of its query per 16-wide k-step.
-  u32x4_t qop[QB][8];
-#pragma unroll
-  for (int qbk = 0; qbk < QB; ++qbk) {
-    const int row = min(q0 + wave * 32 * QB + qbk * 32 + l32, q1 - 1);
+  u32x4_t qop[8];
+  {
+    const int row = min(qrow0 + l32, q1 - 1);
     const u32x4_t* src = (const u32x4_t*)(qb + (size_t)row * 128);
 #pragma unroll
-    for (int ks2 = 0; ks2 < 8; ++ks2) qop[qbk][ks2] = src[ks2 * 2 + h];
+    for (int ks2 = 0; ks2 < 8; ++ks2) qop[ks2] = src[ks2 * 2 + h];
   }
+  f32x16_t acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) acc[db] = f32x16_t{};
+  float m_run = -INFINITY, l_run = 0.0f;
 
-  f32x16_t acc[QB][4];
-#pragma unroll
-  for (int qbk = 0; qbk < QB; ++qbk)
-#pragma unroll
-    for (int db = 0; db < 4; ++db) acc[qbk][db] = f32x16_t{};
-  float m_run[QB], l_run[QB];
-#pragma unroll
-  for (int qbk = 0; qbk < QB; ++qbk) {
-    m_run[qbk] = -INFINITY;
-    l_run[qbk] = 0.0f;
-  }
-
-  // Row table: wave 0 resolves the 64 token rows of an upcoming K or V tile (lane = position) into
-  // rowtab one tile ahead of its use; positions past the stream map to the last valid row (finite
-  // values that the tail mask zeroes).
+  // Row tables: wave 4 resolves K tiles, wave 5 V tiles (lane = tile position).
   const int last_row = seg_start[nseg - 1] + (total - 1 - seg_cum[nseg - 1]);
-  KvCursor kcursor, vcursor;
-  if (wave == 0) {
-    cursor_init(kcursor, seg_start, seg_cum, nseg, min(lane, total - 1));
-    vcursor = kcursor;
-  }
-  auto resolve = [&](KvCursor& cur, int32_t* tab, int t) {
+  KvCursor cursor;
+  if (wave == 4 || wave == 5) cursor_init(cursor, seg_start, seg_cum, nseg, min(lane, total - 1));
+  auto resolve = [&](int32_t* tab, int t) {
     const int p = t * kKT + lane;
-    tab[lane] = p < total ? cursor_row(cur, seg_start, seg_cum, p) : last_row;
+    tab[lane] = p < total ? cursor_row(cursor, seg_start, seg_cum, p) : last_row;
   };
-  // DMA mapping: wave w, group j moves tile rows 4(kDmaIt w + j) + lane/16; lane writes physical
-  // chunk lane%16 of its row, i.e. fetches logical chunk swz(row, lane%16).
+  // DMA mapping (group B): wave 4+w, group j moves tile rows 4(kDmaIt w + j) + lane/16.
   const int prow = lane / 16, pch = lane % 16;
   auto dma = [&](const uint16_t* src, const int32_t* tab, uint16_t* buf) {
 #pragma unroll
     for (int j = 0; j < kDmaIt; ++j) {
-      const int r = 4 * (kDmaIt * wave + j) + prow;
-      lds_dma16(src + (size_t)tab[r] * 128 + swz(r, pch) * 8, buf + 4 * (kDmaIt * wave + j) * 128);
+      const int r = 4 * (kDmaIt * wg + j) + prow;
+      lds_dma16(src + (size_t)tab[r] * 128 + swz(r, pch) * 8, buf + 4 * (kDmaIt * wg + j) * 128);
     }
   };
-  // Lane offsets (bf16 elements) of the swizzled operand reads, loop invariant.
+
   int koffs[8], voffs[2][4];
 #pragma unroll
   for (int ks2 = 0; ks2 < 8; ++ks2) koffs[ks2] = l32 * 128 + swz(l32, ks2 * 2 + h) * 8;
@@ -313,158 +297,169 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       voffs[1][db] = (r0 + 8) * 128 + swz(r0 + 8, c) * 8 + e0;
     }
   }
-  auto scores = [&](const uint16_t* kt, f32x16_t (&sa)[QB][2]) {
-#pragma unroll
-    for (int qbk = 0; qbk < QB; ++qbk) {
-      sa[qbk][0] = f32x16_t{};
-      sa[qbk][1] = f32x16_t{};
-    }
+
+  const int ntiles = (total + kKT - 1) / kKT;
+  f32x16_t sacc[2];
+  u32x4_t pop[2][2];
+
+  auto scores = [&](const uint16_t* kt) {
+    sacc[0] = f32x16_t{};
+    sacc[1] = f32x16_t{};
 #pragma unroll
     for (int ks2 = 0; ks2 < 8; ++ks2) {
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2) {
         const bf16x8_t a = as_bf16x8(*(const u32x4_t*)(&kt[kb2 * 32 * 128 + koffs[ks2]]));
-#pragma unroll
-        for (int qbk = 0; qbk < QB; ++qbk) sa[qbk][kb2] = mfma32x32x16(a, as_bf16x8(qop[qbk][ks2]), sa[qbk][kb2]);
+        sacc[kb2] = mfma32x32x16(a, as_bf16x8(qop[ks2]), sacc[kb2]);
       }
     }
   };
-
-  const int ntiles = (total + kKT - 1) / kKT;
-  f32x16_t sacc[QB][2], sacc2[QB][2];
-  // One tile: kcur holds K(t), knext K(t+1) (refilled with K(t+2)), vcur V(t), vnext (refilled with V(t+1)).
-  auto step = [&](int t, uint16_t* kbuf, const uint16_t* knext, const uint16_t* vbuf, uint16_t* vnext,
-                  f32x16_t (&sacc)[QB][2], f32x16_t (&snext)[QB][2]) {
-    if (t + 2 < ntiles) dma(kb, rowtab[0][t & 1], kbuf);
-    if (t + 1 < ntiles) dma(vb, rowtab[1][(t + 1) & 1], vnext);
-    if (wave == 0) {
-      if (t + 3 < ntiles) resolve(kcursor, rowtab[0][(t + 1) & 1], t + 3);
-      if (t + 2 < ntiles) resolve(vcursor, rowtab[1][t & 1], t + 2);
-    }
-    if (active) {
-      if ((t + 1) * kKT > total) {
-        const int tbase = t * kKT;
+  // MFMA phase M(t): O += V(t)^T P(t)^T, then S(t+1) (if any).
+  auto mphase = [&](int t, const uint16_t* vt, const uint16_t* knext) {
 #pragma unroll
-        for (int qbk = 0; qbk < QB; ++qbk)
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
-          for (int kb2 = 0; kb2 < 2; ++kb2)
+      for (int st = 0; st < 2; ++st) {
+        const int rb = (kb2 * 32 + st * 16) * 128;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
-              if (tbase + key >= total) sacc[qbk][kb2][r] = -INFINITY;
-            }
-      }
-#pragma unroll
-      for (int qbk = 0; qbk < QB; ++qbk) {
-        float mx = sacc[qbk][0][0];
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[qbk][kb2][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
-        if (__any(mx > m_run[qbk] + 8.0f)) {
-          const float m_new = fmaxf(m_run[qbk], mx);
-          const float alpha = __builtin_amdgcn_exp2f(m_run[qbk] - m_new);
-          m_run[qbk] = m_new;
-          l_run[qbk] *= alpha;
-#pragma unroll
-          for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[qbk][db][r] *= alpha;
-        }
-      }
-      // One scheduling region: S(t+1) MFMAs (computed on stale data and discarded after the last
-      // tile) interleaved with the exponentials of S(t), then PV(t).
-      scores(knext, snext);
-      u32x4_t pop[QB][2][2];
-#pragma unroll
-      for (int qbk = 0; qbk < QB; ++qbk) {
-        const float mneg = -m_run[qbk];
-        float ls = 0.0f;
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) {
-          float pv[16];
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[qbk][kb2][r], scale_log2, mneg));
-            ls += pv[r];
-          }
-#pragma unroll
-          for (int st = 0; st < 2; ++st)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) pop[qbk][kb2][st][e] = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
-        }
-        l_run[qbk] += ls;
-      }
-      // O^T += V(t)^T P^T.  Element e of lane (query, h) of the P^T operand is tile key
-      // 16st + 8(e/4) + 4h + e%4 (the score accumulator layout); group grp of the transposed read
-      // gathers rows key0 + gl/4 (key0 = 32kb2 + 16st + 4(grp/2), +8 for elements 4..7) at columns
-      // 32db + 16(grp%2) + 4(gl%4).
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const int rb = (kb2 * 32 + st * 16) * 128;
-#pragma unroll
-          for (int db = 0; db < 4; ++db) {
-            const uint2 lo = ds_read_tr16_b64(&vbuf[rb + voffs[0][db]]);
-            const uint2 hi = ds_read_tr16_b64(&vbuf[rb + voffs[1][db]]);
-            const bf16x8_t a = as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y});
-#pragma unroll
-            for (int qbk = 0; qbk < QB; ++qbk)
-              acc[qbk][db] = mfma32x32x16(a, as_bf16x8(pop[qbk][kb2][st]), acc[qbk][db]);
-          }
+        for (int db = 0; db < 4; ++db) {
+          const uint2 lo = ds_read_tr16_b64(&vt[rb + voffs[0][db]]);
+          const uint2 hi = ds_read_tr16_b64(&vt[rb + voffs[1][db]]);
+          acc[db] = mfma32x32x16(as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y}), as_bf16x8(pop[kb2][st]), acc[db]);
         }
       }
     }
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS DMA has landed
-    __syncthreads();
+    if (t + 1 < ntiles) scores(knext);
+  };
+  // VALU phase V(t): online softmax of S(t) -> bf16 P(t) (per lane: one query, 32 of 64 keys).
+  auto vphase = [&](int t) {
+    if ((t + 1) * kKT > total) {
+      const int tbase = t * kKT;
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+          if (tbase + key >= total) sacc[kb2][r] = -INFINITY;
+        }
+    }
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb2][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+    if (__any(mx > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+    }
+    const float mneg = -m_run;
+    float ls = 0.0f;
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      float pv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][r], scale_log2, mneg));
+        ls += pv[r];
+      }
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pop[kb2][st][e] = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
+    }
+    l_run += ls;
+  };
+  // Group B housekeeping at the start of its V(t): DMA K(t+2), V(t+1); resolve K(t+3), V(t+2).
+  auto fetch = [&](int t, uint16_t* kdst, uint16_t* vdst) {
+    if (t + 2 < ntiles) dma(kb, rowtab[0][t & 1], kdst);
+    if (t + 1 < ntiles) dma(vb, rowtab[1][(t + 1) & 1], vdst);
+    if (wave == 4 && t + 3 < ntiles) resolve(rowtab[0][(t + 1) & 1], t + 3);
+    if (wave == 5 && t + 2 < ntiles) resolve(rowtab[1][t & 1], t + 2);
   };
 
-  // Prologue: row tables of K(0), K(1), V(0); DMA K(0), V(0) -> buffers 0 and K(1) -> K buffer 1;
-  // S(0) while wave 0 resolves K(2) and V(1).
-  if (wave == 0) {
-    resolve(kcursor, rowtab[0][0], 0);
-    if (ntiles > 1) resolve(kcursor, rowtab[0][1], 1);
-    resolve(vcursor, rowtab[1][0], 0);
+  // Prologue: tables K(0), K(1), V(0), V(1); DMA K(0), V(0) -> buffers 0, K(1) -> K buffer 1;
+  // S(0) everywhere, V(0) in group A; table K(2).
+  if (wave == 4) {
+    resolve(rowtab[0][0], 0);
+    if (ntiles > 1) resolve(rowtab[0][1], 1);
+  }
+  if (wave == 5) {
+    resolve(rowtab[1][0], 0);
+    if (ntiles > 1) resolve(rowtab[1][1], 1);
   }
   __syncthreads();
-  dma(kb, rowtab[0][0], k_s0);
-  dma(vb, rowtab[1][0], v_s0);
-  if (ntiles > 1) dma(kb, rowtab[0][1], k_s1);
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (active) scores(k_s0, sacc);
-  if (wave == 0) {
-    if (ntiles > 2) resolve(kcursor, rowtab[0][0], 2);
-    if (ntiles > 1) resolve(vcursor, rowtab[1][1], 1);
+  if (group_b) {
+    dma(kb, rowtab[0][0], k_s0);
+    dma(vb, rowtab[1][0], v_s0);
+    if (ntiles > 1) dma(kb, rowtab[0][1], k_s1);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   __syncthreads();
+  if (active) scores(k_s0);
+  if (active && !group_b) vphase(0);
+  if (wave == 4 && ntiles > 2) resolve(rowtab[0][0], 2);
+  __syncthreads();
+
+  // Half-steps h = 0 .. 2T-1 (unrolled by 4: tile parity fixes the buffers).
+  //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1)        B: h = 2t -> V(t) + fetch;  h = 2t+1 -> M(t)
   for (int t = 0; t < ntiles; t += 2) {
-    step(t, k_s0, k_s1, v_s0, v_s1, sacc, sacc2);
-    if (t + 1 < ntiles) step(t + 1, k_s1, k_s0, v_s1, v_s0, sacc2, sacc);
+    // tile t (even): V(t) in v_s0, K(t+1) in k_s1
+    if (!group_b) {
+      if (active) mphase(t, v_s0, k_s1);
+    } else {
+      fetch(t, k_s0, v_s1);
+      if (active) vphase(t);
+    }
+    __syncthreads();
+    if (!group_b) {
+      if (active && t + 1 < ntiles) vphase(t + 1);
+    } else {
+      if (active) mphase(t, v_s0, k_s1);
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    if (t + 1 >= ntiles) break;
+    // tile t+1 (odd): V(t+1) in v_s1, K(t+2) in k_s0
+    if (!group_b) {
+      if (active) mphase(t + 1, v_s1, k_s0);
+    } else {
+      fetch(t + 1, k_s1, v_s0);
+      if (active) vphase(t + 1);
+    }
+    __syncthreads();
+    if (!group_b) {
+      if (active && t + 2 < ntiles) vphase(t + 2);
+    } else {
+      if (active) mphase(t + 1, v_s1, k_s0);
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
   }
 
   if (!active) return;
   // Normalise and store: lane holds d = db*32 + (r/4)*8 + 4h + r%4 of query l32.
+  const float lt = l_run + __shfl_xor(l_run, 32);
+  const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+  const int row = qrow0 + l32;
+  if (row < q1) {
+    uint16_t* dst = ob + (size_t)row * 128;
 #pragma unroll
-  for (int qbk = 0; qbk < QB; ++qbk) {
-    const float lt = l_run[qbk] + __shfl_xor(l_run[qbk], 32);
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    const int row = q0 + wave * 32 * QB + qbk * 32 + l32;
-    if (row < q1) {
-      uint16_t* dst = ob + (size_t)row * 128;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = db * 32 + g * 8 + h * 4;
-          uint2 w;
-          w.x = cvt_pk_bf16(acc[qbk][db][4 * g] * inv, acc[qbk][db][4 * g + 1] * inv);
-          w.y = cvt_pk_bf16(acc[qbk][db][4 * g + 2] * inv, acc[qbk][db][4 * g + 3] * inv);
-          *(uint2*)(dst + d0) = w;
-        }
-    }
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + g * 8 + h * 4;
+        uint2 w;
+        w.x = cvt_pk_bf16(acc[db][4 * g] * inv, acc[db][4 * g + 1] * inv);
+        w.y = cvt_pk_bf16(acc[db][4 * g + 2] * inv, acc[db][4 * g + 3] * inv);
+        *(uint2*)(dst + d0) = w;
+      }
   }
 }
 
