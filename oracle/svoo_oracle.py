@@ -46,6 +46,9 @@ __all__ = [
     "block_sparse_attention",
     "dense_attention",
     "svoo_attention_call",
+    "hunyuan_post_process",
+    "hunyuan_attention_call",
+    "hunyuan_dense_attention",
 ]
 
 _FIX_SHIFT = 60  # fixed-point scale of the top-p prefix sums (2**60)
@@ -614,3 +617,74 @@ def svoo_attention_call(
         return out, dict(qlabels=ql, klabels=kl, qcentroids=qcent, kcentroids=kcent,
                          qsizes=qsz, ksizes=ksz, map=dmap, qidx=qidx, kidx=kidx)
     return out
+
+
+# --------------------------------------------------------------------------------------
+# HunyuanVideo text-dense variant
+# --------------------------------------------------------------------------------------
+def hunyuan_post_process(dyn_map, q_sizes, k_sizes, q_sorted_idx, video_length: int, context_length: int,
+                         prompt_length: int):
+    """Append the prompt and padding clusters to a video block map.
+
+    Follows ``svoo/models/hunyuan10/attention.py:977-1021``: the map gains two rows and columns;
+    row ``Qc`` (prompt) attends columns ``0..Kc`` (every video cluster and the prompt), column
+    ``Kc`` (prompt) is attended by rows ``0..Qc``, and the padding cluster ``Kc+1`` pairs only with
+    itself.  Sizes gain ``[prompt_length, context_length - prompt_length]``; the query sort order
+    gains the identity over the text tokens.
+    """
+    m = np.asarray(dyn_map, dtype=bool)
+    b, h, qn, kn = m.shape
+    out = np.zeros((b, h, qn + 2, kn + 2), dtype=bool)
+    out[:, :, :qn, :kn] = m
+    out[:, :, qn, : kn + 1] = True      # prompt row: video clusters and the prompt
+    out[:, :, : qn + 1, kn] = True      # prompt column: every video row and the prompt row
+    out[:, :, qn + 1, kn + 1] = True    # padding only with itself
+    tail = np.array([prompt_length, context_length - prompt_length], dtype=np.int64)
+    qs = np.concatenate([np.asarray(q_sizes), np.broadcast_to(tail, (b, h, 2))], axis=-1)
+    ks = np.concatenate([np.asarray(k_sizes), np.broadcast_to(tail, (b, h, 2))], axis=-1)
+    idx = np.asarray(q_sorted_idx)
+    text = np.arange(video_length, video_length + context_length)
+    qidx = np.concatenate([idx, np.broadcast_to(text, (idx.shape[0], context_length))], axis=1)
+    return out, qs, ks, qidx
+
+
+def hunyuan_attention_call(query, key, value, num_q_centroids: int, num_k_centroids: int, kmeans_iters: int,
+                           top_p: float, min_kc_ratio, prompt_length: int, context_length: int, *,
+                           init_q_idx=None, init_k_idx=None, dtype: str = "bf16", attn_dtype=np.float64):
+    """One sparse Hunyuan ``attention_core_logic`` call, output ``[1, H, S, D]``.
+
+    Follows ``svoo/models/hunyuan10/attention.py:1031-1110``: co-cluster the video part (the first
+    ``S - context_length`` tokens), mask it, permute video Q by query labels and video K/V by key
+    labels with the text kept last, extend the map and sizes (:func:`hunyuan_post_process`),
+    block-sparse attention over the whole sequence and the inverse permutation.
+    """
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    v = np.asarray(value, dtype=np.float32)
+    b, h, s, d = q.shape
+    assert b == 1
+    vl = s - context_length
+    qv, kv = q[0, :, :vl], k[0, :, :vl]
+    ql, qcent, qsz, kl, kcent, ksz = co_cluster_tokens(qv, kv, num_q_centroids, num_k_centroids, kmeans_iters,
+                                                       init_q_idx=init_q_idx, init_k_idx=init_k_idx, dtype=dtype)
+    qidx, _, _ = cluster_sort(ql, num_q_centroids)
+    kidx, _, _ = cluster_sort(kl, num_k_centroids)
+    dmap = identify_dynamic_map(qcent[None], kcent[None], qsz[None], ksz[None], top_p, min_kc_ratio, 0, dtype)
+    m2, qs2, ks2, qidx2 = hunyuan_post_process(dmap, qsz[None], ksz[None], qidx, vl, context_length, prompt_length)
+    _, _, _, kidx2 = hunyuan_post_process(dmap, qsz[None], ksz[None], kidx, vl, context_length, prompt_length)
+    qp = permute_rows(q[0], qidx2)
+    kp = permute_rows(k[0], kidx2)
+    vp = permute_rows(v[0], kidx2)
+    op = block_sparse_attention(qp[None], kp[None], vp[None], m2, qs2, ks2, attn_dtype)[0]
+    return unpermute_rows(op, qidx2)[None]
+
+
+def hunyuan_dense_attention(query, key, value, valid_length: int, compute_dtype=np.float64):
+    """The full-precision gate (``svoo/models/hunyuan10/attention.py:1113-1185``): tokens ``< valid_length``
+    attend each other, the rest (prompt padding) attend each other; ``[1, H, S, D]``."""
+    q = np.asarray(query)
+    b, h, s, d = q.shape
+    m = np.zeros((b, h, 2, 2), dtype=bool)
+    m[:, :, 0, 0] = m[:, :, 1, 1] = True
+    sz = np.broadcast_to(np.array([valid_length, s - valid_length]), (b, h, 2))
+    return block_sparse_attention(query, key, value, m, sz, sz, compute_dtype)

@@ -334,3 +334,196 @@ class WanAttn_SAPAttn_Processor:
         out = apply_inverse_permutation_bshd(out_perm, q_sorted_indices)
         self._mark("unpermute")
         return out
+
+
+def _apply_rotary_emb_real(x: torch.Tensor, freqs_cis) -> torch.Tensor:
+    """RoPE with real ``(cos, sin)`` tables of shape ``[S, D]`` on interleaved pairs, ``[B, H, S, D]`` input.
+
+    The rotary form HunyuanVideo uses through diffusers' ``apply_rotary_emb(use_real=True,
+    use_real_unbind_dim=-1)`` (called at ``svoo/models/hunyuan10/attention.py:305-353``).
+    """
+    cos, sin = freqs_cis
+    cos = cos[None, None].to(x.device)
+    sin = sin[None, None].to(x.device)
+    x_real, x_imag = x.reshape(*x.shape[:-1], -1, 2).unbind(-1)
+    x_rot = torch.stack([-x_imag, x_real], dim=-1).flatten(3)
+    return (x.float() * cos + x_rot.float() * sin).to(x.dtype)
+
+
+def _extend_with_text(sorted_indices: torch.Tensor, video_length: int, context_length: int) -> torch.Tensor:
+    """``[BH, V]`` video sort order -> ``[BH, V + C]`` with the text tokens ``V .. V+C-1`` in place
+    (``svoo/models/hunyuan10/attention.py:1013-1017``)."""
+    text = torch.arange(video_length, video_length + context_length, dtype=sorted_indices.dtype,
+                        device=sorted_indices.device)
+    return torch.cat([sorted_indices, text.expand(sorted_indices.shape[0], context_length)], dim=1).contiguous()
+
+
+class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
+    """Semantic-aware-permutation attention for HunyuanVideo (``svoo/models/hunyuan10/attention.py:757-1110``).
+
+    The sequence is ``num_frame * frame_size`` video tokens followed by ``context_length`` text
+    tokens, of which the first ``prompt_length`` are the valid prompt.  The video part is
+    co-clustered, masked and permuted as in Wan; the text stays at the end and becomes two extra
+    clusters (``dynamic_map_post_processing``, ``:977-1021``): the prompt attends every video
+    cluster and itself, every video cluster attends the prompt, and the unused padding attends only
+    itself.  ``attention_core_logic`` returns ``[1, H, S, D]``.
+    """
+
+    prompt_length = 0
+    context_length = 256
+    num_frame = 33
+    frame_size = 3600
+
+    # ---------------------------------------------------------------- diffusers glue (hunyuan10/attention.py:459-575)
+    def get_qkv(self, attn, hidden_states, encoder_hidden_states=None):
+        return attn.to_q(hidden_states), attn.to_k(hidden_states), attn.to_v(hidden_states)
+
+    def get_transpose_qkv(self, attn, query, key, value):
+        t = lambda x: x.unflatten(2, (attn.heads, -1)).transpose(1, 2).contiguous()  # noqa: E731
+        return t(query), t(key), t(value)
+
+    def get_rotary_emb(self, attn, query, key, image_rotary_emb, encoder_hidden_states):
+        if image_rotary_emb is None:
+            return query, key
+        if getattr(attn, "add_q_proj", None) is None and encoder_hidden_states is not None:
+            # Single-stream block: RoPE on the video part, text (last) untouched.
+            txt = encoder_hidden_states.shape[1]
+            query = torch.cat([_apply_rotary_emb_real(query[:, :, :-txt], image_rotary_emb), query[:, :, -txt:]], dim=2)
+            key = torch.cat([_apply_rotary_emb_real(key[:, :, :-txt], image_rotary_emb), key[:, :, -txt:]], dim=2)
+            return query, key
+        return _apply_rotary_emb_real(query, image_rotary_emb), _apply_rotary_emb_real(key, image_rotary_emb)
+
+    def get_encoder_condition_and_concat(self, attn, query, key, value, encoder_hidden_states):
+        if getattr(attn, "add_q_proj", None) is not None and encoder_hidden_states is not None:
+            t = lambda x: x.unflatten(2, (attn.heads, -1)).transpose(1, 2)  # noqa: E731
+            eq = t(attn.add_q_proj(encoder_hidden_states))
+            ek = t(attn.add_k_proj(encoder_hidden_states))
+            ev = t(attn.add_v_proj(encoder_hidden_states))
+            if getattr(attn, "norm_added_q", None) is not None:
+                eq = attn.norm_added_q(eq)
+            if getattr(attn, "norm_added_k", None) is not None:
+                ek = attn.norm_added_k(ek)
+            query = torch.cat([query, eq], dim=2)
+            key = torch.cat([key, ek], dim=2)
+            value = torch.cat([value, ev], dim=2)
+        return query.contiguous(), key.contiguous(), value.contiguous()
+
+    def get_cu_max_seqlen(self, attention_mask, device):
+        """``([0, valid, total]`` for q and kv, max lengths); built on the device (no host read-back)."""
+        mask = attention_mask.to(device)
+        total = mask.numel()
+        cu = torch.zeros(3, dtype=torch.int32, device=device)
+        cu[1] = mask.sum().to(torch.int32)
+        cu[2] = total
+        return cu, cu.clone(), total, total
+
+    def get_o(self, attn, hidden_states, encoder_hidden_states):
+        if encoder_hidden_states is not None:
+            n_txt = encoder_hidden_states.shape[1]
+            hidden_states, encoder_hidden_states = hidden_states[:, :-n_txt], hidden_states[:, -n_txt:]
+            if getattr(attn, "to_out", None) is not None:
+                hidden_states = attn.to_out[0](hidden_states)
+                hidden_states = attn.to_out[1](hidden_states)
+            if getattr(attn, "to_add_out", None) is not None:
+                encoder_hidden_states = attn.to_add_out(encoder_hidden_states)
+        return hidden_states, encoder_hidden_states
+
+    def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, image_rotary_emb=None,
+                 timestep=None):
+        """Diffusers processor entry (``svoo/models/hunyuan10/attention.py:536-575``); returns ``(hidden, encoder_hidden)``."""
+        if getattr(attn, "add_q_proj", None) is None and encoder_hidden_states is not None:
+            hidden_states = torch.cat([hidden_states, encoder_hidden_states], dim=1)
+        query, key, value = self.get_qkv(attn, hidden_states)
+        query, key, value = self.get_transpose_qkv(attn, query, key, value)
+        query, key = self.get_qk_norm(attn, query, key)
+        query, key = self.get_rotary_emb(attn, query, key, image_rotary_emb, encoder_hidden_states)
+        query, key, value = self.get_encoder_condition_and_concat(attn, query, key, value, encoder_hidden_states)
+        if attention_mask is None:
+            attention_mask = torch.ones(query.shape[2], dtype=torch.bool, device=query.device)
+        cu_max_seqlens = self.get_cu_max_seqlen(attention_mask, query.device)
+        out = self.attention_core_logic(query, key, value, timestep, self.layer_idx, cu_max_seqlens)
+        out = out.transpose(1, 2).flatten(2, 3).to(query.dtype)
+        return self.get_o(attn, out, encoder_hidden_states)
+
+    # ---------------------------------------------------------------- attention
+    def flashinfer_attention(self, query, key, value, cu_max_seqlens):
+        """Dense attention of the full-precision gate (``:639-645``, ``:1113-1185``): valid tokens attend each
+        other, the padding attends itself; a 2x2 block map on the same sparse kernel."""
+        cu_q, cu_kv = cu_max_seqlens[0], cu_max_seqlens[1]
+        b, h = query.shape[:2]
+        dev = query.device
+        rs = (cu_q[1:] - cu_q[:-1]).to(device=dev, dtype=torch.int32).repeat(b, h, 1)
+        cs = (cu_kv[1:] - cu_kv[:-1]).to(device=dev, dtype=torch.int32).repeat(b, h, 1)
+        bmap = torch.eye(2, dtype=torch.bool, device=dev).repeat(b, h, 1, 1)
+        return dynamic_block_sparse_fwd(query, key, value, bmap, rs, cs, validate=False)
+
+    flash_attention = flashinfer_attention
+
+    def dynamic_map_post_processing(self, dyn_map, qc_sz, kc_sz, q_sorted_indices, video_length, context_length,
+                                    prompt_length, unprompt_length):
+        """Append the prompt and padding clusters (``:977-1021``), on the device.
+
+        ``dyn_map [B, H, Qc, Kc] -> [B, H, Qc+2, Kc+2]``: row ``Qc`` (prompt) attends key clusters
+        ``0..Kc`` (video and prompt), column ``Kc`` (prompt) is attended by rows ``0..Qc``, row and
+        column ``Kc+1`` (padding) only by each other.  Sizes gain ``[prompt_length, unprompt_length]``;
+        ``q_sorted_indices [BH, V]`` gains the identity over the text tokens.
+        """
+        dyn_map = F.pad(dyn_map, (0, 2, 0, 2), value=False)
+        dyn_map[:, :, -2, :-1] = True
+        dyn_map[:, :, :-1, -2] = True
+        dyn_map[:, :, -1, -1] = True
+        tail = torch.tensor([prompt_length, unprompt_length], dtype=qc_sz.dtype, device=qc_sz.device)
+        qc_sz = torch.cat([qc_sz, tail.expand(*qc_sz.shape[:-1], 2)], dim=-1)
+        kc_sz = torch.cat([kc_sz, tail.to(kc_sz.dtype).expand(*kc_sz.shape[:-1], 2)], dim=-1)
+        return dyn_map, qc_sz, kc_sz, _extend_with_text(q_sorted_indices, video_length, context_length)
+
+    def attention_core_logic(self, query, key, value, timestep, layer_idx=None, cu_max_seqlens=None):
+        """Hunyuan SVOO attention for ``[1, H, S, D]`` Q/K/V (``:1031-1110``); returns ``[1, H, S, D]``."""
+        cfg, num_heads, seq_len, dim = query.size()
+        assert cfg == 1, "Batch size must be 1 for kmeans block sparse attention"
+        prompt_length, context_length = self.prompt_length, self.context_length
+        video_length = self.num_frame * self.frame_size
+        assert seq_len == context_length + video_length, (
+            f"Query Shape: {seq_len} is not equivalent to {context_length} + {self.num_frame} * {self.frame_size}"
+        )
+        self.current_inference_step = getattr(self, "_step_from_callback", None)
+        full = self.layer_idx < self.first_layers_fp
+        if timestep is not None:
+            tval = timestep[0].item() if isinstance(timestep, torch.Tensor) else timestep
+            if tval > self.first_times_fp:
+                full = True
+        if full:
+            if self.zero_step_kmeans_init:
+                self.kmeans_clustering(query[:, :, :video_length].contiguous(), key[:, :, :video_length].contiguous(),
+                                       self.layer_idx)
+            if cu_max_seqlens is None:
+                valid = video_length + prompt_length
+                cu = torch.tensor([0, valid, seq_len], dtype=torch.int32, device=query.device)
+                cu_max_seqlens = (cu, cu, seq_len, seq_len)
+            return self.flashinfer_attention(query, key, value, cu_max_seqlens).reshape(cfg, num_heads, seq_len, dim)
+
+        # 1. Video part: cluster (or reuse), per-head ratios, block mask.
+        q_video = query[:, :, :video_length].contiguous()
+        k_video = key[:, :, :video_length].contiguous()
+        r = self.kmeans_clustering(q_video, k_video, self.layer_idx)
+        del q_video, k_video
+        min_kc_ratio = self._get_min_kc_ratio_for_heads_from_step(self.current_inference_step, num_heads)
+        q_sizes = r["qsizes"].view(cfg, num_heads, self.num_q_centroids)
+        k_sizes = r["ksizes"].view(cfg, num_heads, self.num_k_centroids)
+        dyn_map, lengths = block_mask_lengths(
+            r["qcentroids"].view(cfg, num_heads, self.num_q_centroids, dim),
+            r["kcentroids"].view(cfg, num_heads, self.num_k_centroids, dim),
+            q_sizes, k_sizes, self.top_p_kmeans, min_kc_ratio, self.max_kc_ratio,
+        )
+        # 2. Text clusters; permutes over the whole sequence with the text rows mapped to themselves.
+        unprompt_length = context_length - prompt_length
+        dyn_map, qc_sz, kc_sz, q_idx = self.dynamic_map_post_processing(
+            dyn_map, q_sizes, k_sizes, r["q_sorted_idx"], video_length, context_length, prompt_length, unprompt_length)
+        k_idx = _extend_with_text(r["k_sorted_idx"], video_length, context_length)
+        q_perm = _permute_rows(query.contiguous(), q_idx)
+        k_perm, v_perm = permute_pair_by_indices(key.contiguous(), value.contiguous(), k_idx)
+        self._last_call = dict(clustering=r, map=dyn_map, lengths=lengths, min_kc_ratio=min_kc_ratio)
+        out_perm = dynamic_block_sparse_fwd(q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, validate=False)
+        if self.enable_mem_save:
+            del q_perm, k_perm, v_perm
+        return apply_inverse_permutation(out_perm, q_idx, 2)

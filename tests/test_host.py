@@ -146,3 +146,21 @@ def test_golden_fixture_matches_oracle():
     for ci, (p, mn, mx) in enumerate(MASK_CASES):
         m = O.identify_dynamic_map(qc[None], kc[None], qs[None], ks[None], p, mn, mx)
         np.testing.assert_array_equal(m[0], g[f"map{ci}"])
+
+
+def test_hunyuan_processor_post_processing_matches_oracle():
+    import torch
+
+    from svoo_amd.processor import Hunyuan_SAPAttn_Processor
+
+    r = np.random.default_rng(3)
+    m = r.random((1, 2, 5, 7)) < 0.4
+    qs = r.integers(1, 9, size=(1, 2, 5)).astype(np.int32)
+    ks = r.integers(0, 9, size=(1, 2, 7)).astype(np.int32)
+    idx = np.stack([r.permutation(30) for _ in range(2)]).astype(np.int32)
+    proc = Hunyuan_SAPAttn_Processor(layer_idx=0)
+    got = proc.dynamic_map_post_processing(torch.from_numpy(m), torch.from_numpy(qs), torch.from_numpy(ks),
+                                           torch.from_numpy(idx), 30, 12, 7, 5)
+    want = O.hunyuan_post_process(m, qs, ks, idx, 30, 12, 7)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g.numpy(), w)

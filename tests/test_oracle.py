@@ -263,3 +263,39 @@ def test_attention_call_reduces_to_dense():
     out = O.svoo_attention_call(q, k, v, 1, 1, 2, 1.0, init_q_idx=init, init_k_idx=init)
     dense = O.dense_attention(q, k, v)
     np.testing.assert_allclose(out, np.transpose(dense, (0, 2, 1, 3)).reshape(1, n, h * 128), rtol=1e-9, atol=1e-12)
+
+
+def test_hunyuan_post_process_rules():
+    # 2 video q-clusters x 3 video k-clusters; prompt 5 of 8 text tokens.
+    m = np.array([[[[1, 0, 1], [0, 1, 0]]]], dtype=bool)
+    qs = np.array([[[4, 6]]])
+    ks = np.array([[[3, 3, 4]]])
+    idx = np.array([[3, 1, 0, 2, 4, 5, 9, 8, 7, 6]])
+    m2, qs2, ks2, idx2 = O.hunyuan_post_process(m, qs, ks, idx, 10, 8, 5)
+    expect = np.array([[1, 0, 1, 1, 0],
+                       [0, 1, 0, 1, 0],
+                       [1, 1, 1, 1, 0],
+                       [0, 0, 0, 0, 1]], dtype=bool)
+    np.testing.assert_array_equal(m2[0, 0], expect)
+    np.testing.assert_array_equal(qs2[0, 0], [4, 6, 5, 3])
+    np.testing.assert_array_equal(ks2[0, 0], [3, 3, 4, 5, 3])
+    np.testing.assert_array_equal(idx2[0], [3, 1, 0, 2, 4, 5, 9, 8, 7, 6, 10, 11, 12, 13, 14, 15, 16, 17])
+
+
+def test_hunyuan_dense_gate_closed_form():
+    q, k, v = (RNG.standard_normal((1, 2, 40, 128)) for _ in range(3))
+    out = O.hunyuan_dense_attention(q, k, v, 31)
+    sd = lambda a, b, c: torch.nn.functional.scaled_dot_product_attention(  # noqa: E731
+        torch.from_numpy(a), torch.from_numpy(b), torch.from_numpy(c)).numpy()
+    np.testing.assert_allclose(out[:, :, :31], sd(q[:, :, :31], k[:, :, :31], v[:, :, :31]), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(out[:, :, 31:], sd(q[:, :, 31:], k[:, :, 31:], v[:, :, 31:]), rtol=1e-10, atol=1e-12)
+
+
+def test_hunyuan_call_with_all_blocks_is_dense_varlen():
+    # top_p >= 1 keeps every video block, so video + prompt form one dense block and the padding another.
+    h, vl, ctx, prompt = 2, 96, 16, 11
+    q, k, v = (O.bf16_round(RNG.standard_normal((1, h, vl + ctx, 128)).astype(np.float32)) for _ in range(3))
+    init_q = RNG.integers(0, vl, size=(h, 4))
+    init_k = RNG.integers(0, vl, size=(h, 6))
+    out = O.hunyuan_attention_call(q, k, v, 4, 6, 2, 1.0, 0, prompt, ctx, init_q_idx=init_q, init_k_idx=init_k)
+    np.testing.assert_allclose(out, O.hunyuan_dense_attention(q, k, v, vl + prompt), rtol=1e-9, atol=1e-12)
