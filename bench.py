@@ -79,7 +79,7 @@ def main():
 
     from svoo_amd import _lib, synth
     from svoo_amd.co_clustering import co_cluster_tokens_full
-    from svoo_amd.processor import WanAttn_SAPAttn_Processor
+    from svoo_amd.processor import Hunyuan_SAPAttn_Processor, WanAttn_SAPAttn_Processor
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a HIP device")
@@ -88,8 +88,8 @@ def main():
     cfg = synth.CONFIGS[args.config]
     h, n, d = cfg.heads, cfg.tokens, cfg.head_dim
     qcn, kcn, iters = cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters
-    if cfg.text_tokens:
-        raise SystemExit("text-dense (HunyuanVideo) configs are not benchmarked by this script")
+    hunyuan = cfg.text_tokens > 0
+    nv = cfg.video_tokens
 
     log(f"config {cfg.name}: H={h} N={n} d={d} Qc={qcn} Kc={kcn} iters={iters} mode={args.mode}")
     t0 = time.time()
@@ -105,17 +105,24 @@ def main():
 
     # "Previous step": a clustering from seeded random token indices; the timed calls warm-start
     # from its centroids perturbed by N(0, (0.05 rms)^2).
-    qi = synth.init_indices(cfg, h, qcn, n, 1).to(dev)
-    ki = synth.init_indices(cfg, h, kcn, n, 2).to(dev)
-    prev = co_cluster_tokens_full(q[0], k[0], qcn, kcn, iters, init_q_idx=qi, init_k_idx=ki)
+    qv, kv = (x[0, :, :nv].contiguous() for x in (q, k))
+    qi = synth.init_indices(cfg, h, qcn, nv, 1).to(dev)
+    ki = synth.init_indices(cfg, h, kcn, nv, 2).to(dev)
+    prev = co_cluster_tokens_full(qv, kv, qcn, kcn, iters, init_q_idx=qi, init_k_idx=ki)
+    del qv, kv
     q_init = synth.perturb_centroids(cfg, prev["qcentroids"], 3)
     k_init = synth.perturb_centroids(cfg, prev["kcentroids"], 4)
     del prev
 
-    class Proc(WanAttn_SAPAttn_Processor):
+    class Proc(Hunyuan_SAPAttn_Processor if hunyuan else WanAttn_SAPAttn_Processor):
         pass
 
-    Proc.num_frame, Proc.frame_size, Proc.context_length = cfg.frames, cfg.frame_size, 0
+    Proc.num_frame, Proc.frame_size = cfg.frames, cfg.frame_size
+    Proc.context_length = cfg.text_tokens
+    if hunyuan:
+        # all text tokens are the valid prompt: the padding cluster is empty
+        Proc.prompt_length = cfg.text_tokens
+        Proc.first_times_fp = float("inf")
     Proc.num_q_centroids, Proc.num_k_centroids = qcn, kcn
     Proc.top_p_kmeans, Proc.min_kc_ratio, Proc.max_kc_ratio = top_p, ratios, 0
     Proc.kmeans_iter_init = Proc.kmeans_iter_step = iters
@@ -129,6 +136,8 @@ def main():
         proc._cached_clustering_results = None
         proc.current_inference_step = None
         proc.stage_events = events
+        if hunyuan:
+            return proc.attention_core_logic(q, k, v, 0.0, 0)
         return proc.attention_core_logic(q, k, v, timestep=None)
 
     for _ in range(args.warmup):
@@ -152,22 +161,18 @@ def main():
     t_call_ms = start.elapsed_time(end) / args.steps
     log(f"timed {args.steps} calls: {t_call_ms:.3f} ms/call (host wall {1e3 * wall / args.steps:.3f} ms/call)")
 
-    names = ["cluster", "permute", "mask", "attention", "unpermute"]
-    stage = {nm: [] for nm in names}
+    # stage = time between a mark and the previous one, in the order the call records them
+    stage = {}
     for ev in all_events:
-        marks = dict(ev)
-        prev_name = "start"
-        for nm in names:
-            stage[nm].append(marks[prev_name].elapsed_time(marks[nm]))
-            prev_name = nm
+        for (_, e0), (nm, e1) in zip(ev[:-1], ev[1:]):
+            stage.setdefault(nm, []).append(e0.elapsed_time(e1))
     stages_ms = {nm: float(np.median(vals)) for nm, vals in stage.items()}
     attn_ms_avg = float(np.mean(stage["attention"]))
 
     # Work of the last call (every call starts from the same centroids, so all calls are equal).
     last = proc._last_call
-    r = last["clustering"]
-    qs = r["qsizes"].to(torch.int64).view(1, h, qcn)
-    ks = r["ksizes"].to(torch.int64).view(1, h, kcn)
+    qs = last["q_sizes"].to(torch.int64)
+    ks = last["k_sizes"].to(torch.int64)
     dmap = last["map"]
     pairs = int((dmap.to(torch.int64) * qs[..., :, None] * ks[..., None, :]).sum().item())
     active_flop = 4.0 * d * pairs
@@ -182,14 +187,16 @@ def main():
     proc._step_from_callback = 2
     Proc.start_reuse_step, Proc.reuse_interval = 1, 1000
     proc.stage_events = None
-    proc.attention_core_logic(q, k, v, timestep=None)  # warm-up; reuses the last timed call's clustering
+    call = (lambda: proc.attention_core_logic(q, k, v, 0.0, 0)) if hunyuan else (
+        lambda: proc.attention_core_logic(q, k, v, timestep=None))
+    call()  # warm-up; reuses the last timed call's clustering
     assert proc.should_recluster() is False
     torch.cuda.synchronize()
     rs, re_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     nreuse = max(3, args.steps // 2)
     rs.record()
     for _ in range(nreuse):
-        proc.attention_core_logic(q, k, v, timestep=None)
+        call()
     re_.record()
     torch.cuda.synchronize()
     reuse_ms = rs.elapsed_time(re_) / nreuse
@@ -242,7 +249,7 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, args.cpu_heads, t_call_ms)
+        cpu = cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, args.cpu_heads, t_call_ms, hunyuan)
 
     line = {
         "metric": METRIC,
@@ -266,6 +273,7 @@ def main():
         "latency_ms": round(t_call_ms, 4),
         "reuse_step_ms": round(reuse_ms, 4),
         "stages_ms": {kk: round(vv, 4) for kk, vv in stages_ms.items()},
+        "text_tokens": cfg.text_tokens,
         "realized_density": round(realized_density, 5),
         "active_tflops": round(active_tflops, 2),
         "permute_gbps": round(permute_bytes / (permute_ms * 1e-3) / 1e9, 1),
@@ -278,7 +286,7 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms):
+def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms, hunyuan=False):
     """The numpy oracle on ``nheads`` heads of the same inputs; latency scaled linearly to all heads."""
     import numpy as np
 
@@ -292,8 +300,13 @@ def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms)
     ki = k_init.view(h, -1, d)[sel].float().cpu().numpy()
     rs = [ratios[i] for i in sel]
     t0 = time.perf_counter()
-    O.svoo_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
-                          init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
+    if hunyuan:
+        O.hunyuan_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
+                                 cfg.text_tokens, cfg.text_tokens, init_q_centroids=qi, init_k_centroids=ki,
+                                 attn_dtype=np.float32)
+    else:
+        O.svoo_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
+                              init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
     t = time.perf_counter() - t0
     per_head = t / nheads
     call_s = per_head * h

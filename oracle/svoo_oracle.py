@@ -650,7 +650,8 @@ def hunyuan_post_process(dyn_map, q_sizes, k_sizes, q_sorted_idx, video_length: 
 
 def hunyuan_attention_call(query, key, value, num_q_centroids: int, num_k_centroids: int, kmeans_iters: int,
                            top_p: float, min_kc_ratio, prompt_length: int, context_length: int, *,
-                           init_q_idx=None, init_k_idx=None, dtype: str = "bf16", attn_dtype=np.float64):
+                           init_q_idx=None, init_k_idx=None, init_q_centroids=None, init_k_centroids=None,
+                           dtype: str = "bf16", attn_dtype=np.float64):
     """One sparse Hunyuan ``attention_core_logic`` call, output ``[1, H, S, D]``.
 
     Follows ``svoo/models/hunyuan10/attention.py:1031-1110``: co-cluster the video part (the first
@@ -666,7 +667,9 @@ def hunyuan_attention_call(query, key, value, num_q_centroids: int, num_k_centro
     vl = s - context_length
     qv, kv = q[0, :, :vl], k[0, :, :vl]
     ql, qcent, qsz, kl, kcent, ksz = co_cluster_tokens(qv, kv, num_q_centroids, num_k_centroids, kmeans_iters,
-                                                       init_q_idx=init_q_idx, init_k_idx=init_k_idx, dtype=dtype)
+                                                       init_q_idx=init_q_idx, init_k_idx=init_k_idx,
+                                                       init_q_centroids=init_q_centroids,
+                                                       init_k_centroids=init_k_centroids, dtype=dtype)
     qidx, _, _ = cluster_sort(ql, num_q_centroids)
     kidx, _, _ = cluster_sort(kl, num_k_centroids)
     dmap = identify_dynamic_map(qcent[None], kcent[None], qsz[None], ksz[None], top_p, min_kc_ratio, 0, dtype)

@@ -241,8 +241,11 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   int32_t* seg_start = seg_mem;
   int32_t* seg_cum = seg_mem + kn;
   int total = 0;
-  const int nseg = build_segments(map + ((size_t)b * qn + ci) * kn, koff + (size_t)b * (kn + 1), ks + (size_t)b * kn,
+  const int nseg_v = build_segments(map + ((size_t)b * qn + ci) * kn, koff + (size_t)b * (kn + 1), ks + (size_t)b * kn,
                                   kn, seg_start, seg_cum, red, &total);
+  // Segment count and stream length are block-uniform: keep them scalar so tile-loop branches are uniform.
+  const int nseg = __builtin_amdgcn_readfirstlane(nseg_v);
+  total = __builtin_amdgcn_readfirstlane(total);
 
   if (total == 0) {
     // Empty row: zero output (reference semantics, svoo/co_clustering.py:1102-1104).

@@ -290,7 +290,8 @@ class WanAttn_SAPAttn_Processor:
             r["kcentroids"].view(cfg, num_heads, self.num_k_centroids, dim),
             q_sizes, k_sizes, self.top_p_kmeans, min_kc_ratio, self.max_kc_ratio,
         )
-        self._last_call = dict(clustering=r, map=dynamic_map, lengths=lengths, min_kc_ratio=min_kc_ratio)
+        self._last_call = dict(clustering=r, map=dynamic_map, lengths=lengths, min_kc_ratio=min_kc_ratio,
+                               q_sizes=q_sizes, k_sizes=k_sizes)
         return q_perm, k_perm, v_perm, dynamic_map, q_sizes, k_sizes, r["q_sorted_idx"]
 
     def attention_core_logic(self, query, key, value, timestep):
@@ -503,10 +504,12 @@ class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
             return self.flashinfer_attention(query, key, value, cu_max_seqlens).reshape(cfg, num_heads, seq_len, dim)
 
         # 1. Video part: cluster (or reuse), per-head ratios, block mask.
+        self._mark("start")
         q_video = query[:, :, :video_length].contiguous()
         k_video = key[:, :, :video_length].contiguous()
         r = self.kmeans_clustering(q_video, k_video, self.layer_idx)
         del q_video, k_video
+        self._mark("cluster")
         min_kc_ratio = self._get_min_kc_ratio_for_heads_from_step(self.current_inference_step, num_heads)
         q_sizes = r["qsizes"].view(cfg, num_heads, self.num_q_centroids)
         k_sizes = r["ksizes"].view(cfg, num_heads, self.num_k_centroids)
@@ -515,6 +518,7 @@ class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
             r["kcentroids"].view(cfg, num_heads, self.num_k_centroids, dim),
             q_sizes, k_sizes, self.top_p_kmeans, min_kc_ratio, self.max_kc_ratio,
         )
+        self._mark("mask")
         # 2. Text clusters; permutes over the whole sequence with the text rows mapped to themselves.
         unprompt_length = context_length - prompt_length
         dyn_map, qc_sz, kc_sz, q_idx = self.dynamic_map_post_processing(
@@ -522,8 +526,13 @@ class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
         k_idx = _extend_with_text(r["k_sorted_idx"], video_length, context_length)
         q_perm = _permute_rows(query.contiguous(), q_idx)
         k_perm, v_perm = permute_pair_by_indices(key.contiguous(), value.contiguous(), k_idx)
-        self._last_call = dict(clustering=r, map=dyn_map, lengths=lengths, min_kc_ratio=min_kc_ratio)
+        self._mark("permute")
+        self._last_call = dict(clustering=r, map=dyn_map, lengths=lengths, min_kc_ratio=min_kc_ratio,
+                               q_sizes=qc_sz, k_sizes=kc_sz)
         out_perm = dynamic_block_sparse_fwd(q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, validate=False)
+        self._mark("attention")
         if self.enable_mem_save:
             del q_perm, k_perm, v_perm
-        return apply_inverse_permutation(out_perm, q_idx, 2)
+        out = apply_inverse_permutation(out_perm, q_idx, 2)
+        self._mark("unpermute")
+        return out
