@@ -43,7 +43,8 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="C3", choices=["C2", "C3", "C4"])
+    ap.add_argument("--config", default="C3", choices=["C2", "C3", "C4", "C5"],
+                    help="C2-C4: one SVOO attention call; C5: one denoising step of a random-init Wan2.1-1.3B DiT")
     ap.add_argument("--mode", default="density", choices=["density", "reference"],
                     help="density: top_p=0, min_kc_ratio=rho_h; reference: top_p=0.9, min_kc_ratio=clip(rho_h,0.15,0.2)")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
@@ -73,6 +74,9 @@ def main():
         print("bench.py measures one GPU only: the SVOO call is per-head independent and this build runs on "
               "a single MI355X (multi-GPU sharding is design-only); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.config == "C5":
+        return main_dit(args)
 
     import numpy as np
     import torch
@@ -284,6 +288,230 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def main_dit(args):
+    """C5: denoising steps of a random-init Wan2.1-T2V-1.3B-shaped DiT (30 blocks, dim 1536, 12 heads, FFN 8960,
+    480x832x81 video -> N = 21 x 30 x 52 = 32760 tokens) with the SVOO processor in every block's self-attention,
+    installed by ``replace_wan_attention`` with the reference launcher's 1.3B settings (Qc=256, Kc=1024, 2 k-means
+    iterations per clustering).  The per-(step, layer, head) profile is synthetic, rho ~ U[0.05, 0.4], read through
+    ``SparsityLookup`` from a CSV.  Centroids are carried from step to step (warm start).  Three kinds of step are
+    timed: a re-clustering step, a reuse step (clustering cached) and the same DiT with dense SDPA self-attention."""
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from svoo_amd import _lib, dit
+    from svoo_amd.inference import replace_wan_attention
+    from svoo_amd.processor import WanAttn_SAPAttn_Processor
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a HIP device")
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    cfg = dit.WanDiTConfig()
+    height, width, frames = 480, 832, 81
+    t0 = time.time()
+    pipe = dit.make_pipe(cfg, device=dev, dtype=torch.bfloat16, seed=5)
+    model = pipe.transformer
+    g = torch.Generator(device=dev).manual_seed(5)
+    lat = torch.randn(dit.latent_shape(cfg, height, width, frames), generator=g, device=dev).to(torch.bfloat16)
+    txt = torch.randn(1, 512, cfg.text_dim, generator=g, device=dev).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    log(f"C5 DiT built ({sum(p.numel() for p in model.parameters()) / 1e9:.2f} B params) in {time.time() - t0:.1f}s")
+
+    nsteps = args.warmup + 2 * args.steps + 4  # every step the run takes has a profile row
+    layers, heads = cfg.num_layers, cfg.num_attention_heads
+    rho = np.random.default_rng(5).uniform(0.05, 0.4, size=(nsteps + 1, layers, heads))
+    if args.mode == "density":
+        top_p, dmin, dmax = 0.0, None, None
+    else:
+        top_p, dmin, dmax = 0.9, 0.15, 0.20
+
+    class Proc(WanAttn_SAPAttn_Processor):
+        kmeans_warm_start = True
+
+    with tempfile.TemporaryDirectory() as tdir:
+        csv = Path(tdir) / "profile.csv"
+        with open(csv, "w") as f:
+            f.write("Step,Layer,Head,Sparsity\n")
+            for st in range(nsteps + 1):
+                for ly in range(layers):
+                    for hd in range(heads):
+                        f.write(f"{st + 1},{ly},{hd},{rho[st, ly, hd]:.4f}\n")
+        procs = replace_wan_attention(
+            pipe, height, width, frames, first_layers_fp=0, first_times_fp=1000.0, num_q_centroids=256,
+            num_k_centroids=1024, top_p_kmeans=top_p, min_kc_ratio=0.10, kmeans_iter_init=2, kmeans_iter_step=2,
+            start_reuse_step=None, reuse_interval=1, use_dynamic_min_kc_ratio=True, sparsity_csv_path=str(csv),
+            dynamic_min_kc_ratio_min=dmin, dynamic_min_kc_ratio_max=dmax, processor_cls=Proc)
+    n = Proc.num_frame * Proc.frame_size
+    assert n == 32760, n
+    timesteps = iter(np.linspace(999.0, 600.0, 10 * nsteps))
+
+    def fwd(events=False):
+        for p in procs:
+            p.stage_events = [] if events else None
+        t = torch.tensor([float(next(timesteps))], device=dev)
+        with torch.no_grad():
+            return model(lat, t, txt)
+
+    def timed(k, events=False):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        calls = []
+        for _ in range(k):
+            fwd(events)
+            if events:
+                calls.append([p.stage_events for p in procs])
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / k, calls
+
+    for _ in range(args.warmup):
+        fwd()
+    torch.cuda.synchronize()
+    log("warmup done")
+    # re-clustering steps (2 warm-started iterations per block), stage events on every block
+    t_step, calls = timed(args.steps, events=True)
+    call_ms = [ev[0][1].elapsed_time(ev[-1][1]) for step in calls for ev in step]
+    stage = {}
+    for step in calls:
+        for ev in step:
+            for (_, e0), (nm, e1) in zip(ev[:-1], ev[1:]):
+                stage.setdefault(nm, []).append(e0.elapsed_time(e1))
+    stages_ms = {nm: float(np.sum(v)) / args.steps for nm, v in stage.items()}
+    svoo_ms = float(np.sum(call_ms)) / args.steps
+    pairs = 0
+    for p in procs:
+        lc = p._last_call
+        qs, ks = lc["q_sizes"].to(torch.int64), lc["k_sizes"].to(torch.int64)
+        pairs += int((lc["map"].to(torch.int64) * qs[..., :, None] * ks[..., None, :]).sum().item())
+    density = pairs / (layers * heads * float(n) ** 2)
+    log(f"re-clustering step {t_step:.2f} ms (SVOO calls {svoo_ms:.2f} ms over {layers} blocks)")
+
+    # reuse steps: the clustering of the last step is reused by every block
+    Proc.start_reuse_step, Proc.reuse_interval = procs[0].current_inference_step + 1, 10 ** 6
+    fwd()
+    t_reuse, _ = timed(args.steps)
+    assert not any(p.should_recluster() for p in procs)
+    log(f"reuse step {t_reuse:.2f} ms")
+
+    t_dense = None
+    if not args.no_dense:
+        for b in model.blocks:
+            b.attn1.set_processor(dit.DenseWanAttnProcessor())
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            fwd()
+            t_dense, _ = timed(max(2, args.steps // 2))
+        log(f"dense step {t_dense:.2f} ms")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_dit(model, lat, txt, rho, top_p, dmin, dmax, args.cpu_heads, t_step, dev)
+
+    line = {
+        "metric": "Wan2.1-1.3B DiT denoising-step latency with SVOO self-attention (ms), 1 GPU",
+        "value": round(t_step, 3),
+        "unit": "ms per denoising step (re-clustering step)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, Gaussian latents and text embeddings, U[0.05,0.4] profile)",
+        "config": {
+            "workload": f"C5-wan2.1-1.3B-dit-step: 30 blocks, dim 1536, 12 heads, FFN 8960, N={n}, 512 text tokens, "
+                        f"Qc=256 Kc=1024, 2 warm-started k-means iterations per block, {args.mode} mask mode",
+            "layers": layers, "heads": heads, "tokens": n, "q_clusters": 256, "k_clusters": 1024,
+            "kmeans_iters": 2, "top_p": top_p, "mask_mode": args.mode,
+        },
+        "reuse_step_ms": round(t_reuse, 3),
+        "dense_step_ms": None if t_dense is None else round(t_dense, 3),
+        "speedup_vs_dense": None if t_dense is None else round(t_dense / t_step, 3),
+        "reuse_speedup_vs_dense": None if t_dense is None else round(t_dense / t_reuse, 3),
+        "svoo_calls_ms": round(svoo_ms, 3),
+        "stages_ms": {kk: round(vv, 3) for kk, vv in stages_ms.items()},
+        "realized_density": round(density, 5),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_dit(model, lat, txt, rho, top_p, dmin, dmax, nheads, t_step_ms, dev):
+    """One block of the same DiT on the host in float32, its self-attention through the numpy oracle on
+    ``nheads`` heads (scaled to all heads); the block time is scaled by the number of blocks."""
+    import copy
+
+    import numpy as np
+    import torch
+
+    from oracle import svoo_oracle as O
+    from svoo_amd import dit
+
+    cfg = model.config
+    heads, d = cfg.num_attention_heads, cfg.attention_head_dim
+    with torch.no_grad():
+        x = model.patch_embedding(lat).flatten(2).transpose(1, 2).float().cpu()
+        wdt = model.time_embedder[0].weight.dtype
+        temb = model.time_embedder(dit.timestep_embedding(torch.tensor([700.0], device=dev), cfg.freq_dim).to(wdt))
+        tproj = model.time_proj(temb).unflatten(1, (6, -1)).float().cpu()
+        ctx = model.text_embedder(txt).float().cpu()
+        f, hh, ww = lat.shape[2], lat.shape[3] // 2, lat.shape[4] // 2
+        rot = tuple(t.cpu() for t in dit.rope_tables(cfg, f, hh, ww, "cpu"))
+    block = copy.deepcopy(model.blocks[0]).float().cpu()
+    ratios = [float(r) for r in rho[0, 0]]
+    if dmin is not None:
+        ratios = [min(max(r, dmin), dmax) for r in ratios]
+    timing = {}
+
+    class OracleProc:
+        def __call__(self, attn, hidden_states, encoder_hidden_states=None, attention_mask=None, rotary_emb=None,
+                     timestep=None):
+            q = attn.norm_q(attn.to_q(hidden_states)).unflatten(2, (attn.heads, -1))
+            k = attn.norm_k(attn.to_k(hidden_states)).unflatten(2, (attn.heads, -1))
+            v = attn.to_v(hidden_states).unflatten(2, (attn.heads, -1))
+            q, k = dit.apply_rope(q, *rotary_emb), dit.apply_rope(k, *rotary_emb)
+            sel = list(range(nheads))
+            qn, kn, vn = (t.transpose(1, 2)[:, sel].numpy() for t in (q, k, v))
+            n = qn.shape[2]
+            r = np.random.default_rng(0)
+            t0 = time.perf_counter()
+            o = O.svoo_attention_call(qn, kn, vn, 256, 1024, 2, top_p, ratios[:nheads],
+                                      init_q_idx=r.integers(0, n, (nheads, 256)),
+                                      init_k_idx=r.integers(0, n, (nheads, 1024)), attn_dtype=np.float32)
+            timing["attn"] = time.perf_counter() - t0
+            out = torch.zeros(1, n, heads * d)
+            out[..., : nheads * d] = torch.from_numpy(np.asarray(o, np.float32)).reshape(1, n, nheads * d)
+            return attn.to_out[0](out)
+
+    block.attn1.set_processor(OracleProc())
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        block(x, ctx, tproj, rot, timestep=None)
+    t_block = time.perf_counter() - t0
+    t_rest = t_block - timing["attn"]
+    t_block_scaled = t_rest + timing["attn"] * heads / nheads
+    step_s = t_block_scaled * cfg.num_layers
+    log(f"CPU: block {t_block:.1f}s (oracle attention {timing['attn']:.1f}s for {nheads} head(s)) -> "
+        f"{step_s:.0f}s per step")
+    return {
+        "value": round(step_s * 1e3, 1),
+        "unit": "ms per denoising step",
+        "cores": cpu_threads(),
+        "kind": "port",
+        "sample": f"block 0 on the host in float32 (torch for projections, norms, cross-attention and FFN; the numpy "
+                  f"oracle for the SVOO self-attention on {nheads} of {heads} heads): {t_block:.1f} s, attention "
+                  f"scaled x{heads / nheads:g}, block scaled x{cfg.num_layers} = {step_s:.0f} s per step = "
+                  f"{step_s * 1e3 / t_step_ms:.0f}x the GPU step",
+        "step_s_scaled": round(step_s, 1),
+    }
 
 
 def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms, hunyuan=False):

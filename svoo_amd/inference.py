@@ -1,0 +1,118 @@
+"""Install the SVOO attention processors into a Wan pipeline (the reference's configuration surface).
+
+``replace_wan_attention`` follows ``svoo/models/wan/inference.py:23-369`` (SAP branch): it derives the
+token geometry from the pipeline, writes the SVOO configuration as class attributes of
+:class:`WanAttn_SAPAttn_Processor` (shared by every layer, as in the reference) and registers one
+processor instance per transformer block (``transformer_2`` too, for Wan2.2).  The pipeline is
+duck-typed: ``pipe.transformer.blocks[i].attn1.set_processor``, ``pipe.transformer.config``
+(``patch_size``, ``num_attention_heads``, ``attention_head_dim``) and ``pipe.vae_scale_factor_*``.
+No kernel warm-up is needed: the HIP kernels are compiled ahead of time.
+"""
+
+from __future__ import annotations
+
+from .processor import WanAttn_SAPAttn_Processor
+from .sparsity import SparsityLookup
+
+
+def wan_token_geometry(pipe, height: int, width: int, num_frames: int):
+    """``(num_frame_patches, frame_patches_one_frame)`` of a Wan pipeline (``inference.py:81-83``)."""
+    patch = pipe.transformer.config.patch_size
+    num_frame_patches = 1 + num_frames // (pipe.vae_scale_factor_temporal * patch[0])
+    mod_value = pipe.vae_scale_factor_spatial * patch[1]
+    frame_patches_one_frame = int(height // mod_value) * int(width // mod_value)
+    return num_frame_patches, frame_patches_one_frame
+
+
+def replace_wan_attention(
+    pipe,
+    height,
+    width,
+    num_frames,
+    first_layers_fp,
+    first_times_fp,
+    num_inference_steps=None,
+    attention_backend="flexattn",
+    pattern="SAP",
+    num_q_centroids=None,
+    num_k_centroids=None,
+    top_p_kmeans=None,
+    min_kc_ratio=0,
+    max_kc_ratio=0,
+    kmeans_iter_init=0,
+    kmeans_iter_step=0,
+    zero_step_kmeans_init=False,
+    use_global_constraints=False,
+    use_routing_transformer_strategy=False,
+    use_svoo=True,
+    start_reuse_step=None,
+    reuse_interval=1,
+    use_dynamic_min_kc_ratio=False,
+    sparsity_csv_path=None,
+    dynamic_min_kc_ratio_min=None,
+    dynamic_min_kc_ratio_max=None,
+    processor_cls=WanAttn_SAPAttn_Processor,
+    **unused,
+):
+    """Configure SVOO attention and install one processor per Wan DiT block.
+
+    Arguments keep the reference's names and meaning (``svoo/models/wan/inference.py:23-74``);
+    ``first_layers_fp`` is a layer count and ``first_times_fp`` a timestep threshold, as the CLI
+    passes them.  ``max_kc_ratio`` is forwarded to the mask.  Only the SVOO ``"SAP"`` pattern is
+    built here: other patterns raise ``ValueError`` as the reference does for unsupported ones, and
+    the EAR / global-constraint / routing variants raise ``NotImplementedError``.  A missing or
+    unreadable profile CSV disables the dynamic ratios (``:308-320``).  Returns the processors.
+    """
+    if pattern != "SAP" or not use_svoo:
+        raise ValueError("Only the SVOO SAP pattern is supported by this build (pattern='SAP', use_svoo=True).")
+    if use_global_constraints or use_routing_transformer_strategy:
+        raise NotImplementedError("global-constraint and routing-transformer variants are not built here")
+    num_frame_patches, frame_patches_one_frame = wan_token_geometry(pipe, height, width, num_frames)
+    blocks = pipe.transformer.blocks
+    num_layers = len(blocks)
+
+    cls = processor_cls
+    cls.first_layers_fp = first_layers_fp
+    cls.first_times_fp = first_times_fp
+    cls.context_length = 0
+    cls.num_frame = num_frame_patches
+    cls.frame_size = frame_patches_one_frame
+    cls.num_q_centroids = num_q_centroids
+    cls.num_k_centroids = num_k_centroids
+    cls.top_p_kmeans = top_p_kmeans
+    cls.min_kc_ratio = min_kc_ratio
+    cls.max_kc_ratio = max_kc_ratio
+    cls.num_layers = num_layers
+    cls.kmeans_iter_init = kmeans_iter_init
+    cls.kmeans_iter_step = kmeans_iter_step
+    cls.zero_step_kmeans_init = zero_step_kmeans_init
+    cls.use_svoo = True
+    cls.start_reuse_step = start_reuse_step
+    cls.reuse_interval = reuse_interval
+    cls.use_dynamic_min_kc_ratio = False
+    cls.sparsity_lookup = None
+    # a fresh step counter for this pipeline (the class-level state the processors share)
+    cls._current_internal_timestep = None
+    cls._inference_step_counter = 0
+    cls._seen_timesteps = set()
+    if use_dynamic_min_kc_ratio and sparsity_csv_path:
+        try:
+            cls.sparsity_lookup = SparsityLookup(sparsity_csv_path)
+            cls.use_dynamic_min_kc_ratio = True
+            cls.dynamic_min_kc_ratio_min = dynamic_min_kc_ratio_min
+            cls.dynamic_min_kc_ratio_max = dynamic_min_kc_ratio_max
+        except Exception:  # the reference silently falls back to the scalar ratio
+            cls.use_dynamic_min_kc_ratio = False
+            cls.sparsity_lookup = None
+
+    processors = []
+    for transformer in (pipe.transformer, getattr(pipe, "transformer_2", None)):
+        if transformer is None:
+            continue
+        for layer_idx, block in enumerate(transformer.blocks):
+            if hasattr(block.attn1, "set_processor"):
+                proc = cls(layer_idx=layer_idx)
+                proc.num_layers = num_layers
+                block.attn1.set_processor(proc)
+                processors.append(proc)
+    return processors

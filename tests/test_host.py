@@ -164,3 +164,76 @@ def test_hunyuan_processor_post_processing_matches_oracle():
     want = O.hunyuan_post_process(m, qs, ks, idx, 30, 12, 7)
     for g, w in zip(got, want):
         np.testing.assert_array_equal(g.numpy(), w)
+
+
+def _tiny_pipe(layers=2, with_second=False):
+    from svoo_amd import dit
+
+    cfg = dit.WanDiTConfig(num_attention_heads=2, ffn_dim=64, num_layers=layers, text_dim=32)
+    pipe = dit.make_pipe(cfg, dtype=torch.float32)
+    if with_second:
+        pipe.transformer_2 = dit.make_pipe(cfg, dtype=torch.float32, seed=6).transformer
+    return pipe
+
+
+def test_replace_wan_attention_configures_and_installs():
+    from svoo_amd.inference import replace_wan_attention, wan_token_geometry
+    from svoo_amd.processor import WanAttn_SAPAttn_Processor
+
+    pipe = _tiny_pipe(layers=3, with_second=True)
+    # inference.py:81-83: 81 frames, 480x832 -> 21 latent frames of 30x52 patches
+    assert wan_token_geometry(pipe, 480, 832, 81) == (21, 1560)
+    cls = type("P", (WanAttn_SAPAttn_Processor,), {})
+    procs = replace_wan_attention(
+        pipe, 480, 832, 81, first_layers_fp=1, first_times_fp=900, num_q_centroids=100, num_k_centroids=500,
+        top_p_kmeans=0.9, min_kc_ratio=0.1, kmeans_iter_init=2, kmeans_iter_step=2, start_reuse_step=11,
+        reuse_interval=20, use_dynamic_min_kc_ratio=True,
+        sparsity_csv_path=str(GOLDEN / "sparsity_wan_1.3B_t2v_steps1-3.csv"),
+        dynamic_min_kc_ratio_min=0.15, dynamic_min_kc_ratio_max=0.2, processor_cls=cls)
+    assert len(procs) == 6  # both transformers
+    for t in (pipe.transformer, pipe.transformer_2):
+        assert [b.attn1.processor.layer_idx for b in t.blocks] == [0, 1, 2]
+        assert all(isinstance(b.attn1.processor, cls) for b in t.blocks)
+        assert not any(isinstance(b.attn2.processor, cls) for b in t.blocks)  # cross-attention stays dense
+    assert (cls.num_frame, cls.frame_size, cls.context_length, cls.num_layers) == (21, 1560, 0, 3)
+    assert (cls.num_q_centroids, cls.num_k_centroids, cls.top_p_kmeans, cls.min_kc_ratio) == (100, 500, 0.9, 0.1)
+    assert (cls.start_reuse_step, cls.reuse_interval, cls.first_layers_fp, cls.first_times_fp) == (11, 20, 1, 900)
+    assert cls.use_dynamic_min_kc_ratio and cls.sparsity_lookup is not None
+    p = procs[4]
+    assert p._get_min_kc_ratio_for_heads_from_step(2, 12) == [
+        min(max(v, 0.15), 0.2) for v in cls.sparsity_lookup.get_sparsity_batch(2, 1, 12)]
+    # the base class is untouched
+    assert WanAttn_SAPAttn_Processor.num_frame == 0
+
+
+def test_replace_wan_attention_fallbacks_and_rejections():
+    from svoo_amd.inference import replace_wan_attention
+    from svoo_amd.processor import WanAttn_SAPAttn_Processor
+
+    pipe = _tiny_pipe()
+    cls = type("P", (WanAttn_SAPAttn_Processor,), {})
+    replace_wan_attention(pipe, 480, 832, 81, 0, 900, num_q_centroids=8, num_k_centroids=16, top_p_kmeans=0.9,
+                          min_kc_ratio=0.1, use_dynamic_min_kc_ratio=True,
+                          sparsity_csv_path=str(GOLDEN / "missing.csv"), processor_cls=cls)
+    assert not cls.use_dynamic_min_kc_ratio and cls.sparsity_lookup is None  # unreadable profile -> scalar ratio
+    with pytest.raises(ValueError):
+        replace_wan_attention(pipe, 480, 832, 81, 0, 900, pattern="SVG", processor_cls=cls)
+    with pytest.raises(ValueError):
+        replace_wan_attention(pipe, 480, 832, 81, 0, 900, use_svoo=False, processor_cls=cls)
+    with pytest.raises(NotImplementedError):
+        replace_wan_attention(pipe, 480, 832, 81, 0, 900, use_global_constraints=True, processor_cls=cls)
+
+
+def test_tiny_dit_dense_forward_shapes():
+    from svoo_amd import dit
+
+    pipe = _tiny_pipe()
+    cfg = pipe.transformer.config
+    lat = torch.randn(dit.latent_shape(cfg, 64, 96, 9))
+    with torch.no_grad():
+        out = pipe.transformer(lat, torch.tensor([900.0]), torch.randn(1, 8, cfg.text_dim))
+    assert out.shape == lat.shape and torch.isfinite(out).all()
+    cos, sin = dit.rope_tables(cfg, 3, 4, 6, "cpu")
+    assert cos.shape == (1, 72, 1, 128)
+    # pairs share one angle; the t-axis channels of token 0 (position 0) do not rotate
+    assert torch.equal(cos[..., 0::2], cos[..., 1::2]) and torch.all(cos[0, 0, 0] == 1)
