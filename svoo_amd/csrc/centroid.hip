@@ -1,18 +1,19 @@
 // Centroid update over cluster-sorted tokens.
 //
-// accumulate: each wave owns 256 consecutive sorted positions.  Labels are non-decreasing along
+// accumulate: each wave owns 128 consecutive sorted positions.  Labels are non-decreasing along
 //   sorted positions, so the wave walks its rows in order, keeping two fp64 partial sums per lane
 //   (lane l owns dims 2l, 2l+1 of a 128-dim row) and flushing them with one fp64 atomicAdd per
 //   lane whenever the label changes.  Sums of bf16 values are exact in fp64, so the result does
-//   not depend on the order of the atomics.  Rows are fetched 8 at a time for memory parallelism.
+//   not depend on the order of the atomics.  The wave's indices and labels arrive in two vector
+//   loads; rows are then fetched 16 at a time, one batch ahead of the accumulation.
 // finalize: centroid = bf16(f32(sum) / f32(size)), size 0 keeps the old centroid; the sum buffer
 //   is cleared on the way out so the next update starts from zero.
 #include "svoo_common.h"
 
 namespace svoo {
 
-constexpr int kCentPosPerWave = 128;
-constexpr int kCentUnroll = 8;
+constexpr int kCentPosPerWave = 128;  // two index words per lane
+constexpr int kCentBatch = 16;        // rows in flight per wave (double buffered)
 
 __global__ void __launch_bounds__(256) centroid_accumulate_kernel(const uint32_t* __restrict__ x,
                                                                   const int32_t* __restrict__ sorted_idx,
@@ -23,37 +24,54 @@ __global__ void __launch_bounds__(256) centroid_accumulate_kernel(const uint32_t
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int p0 = (blockIdx.x * (blockDim.x / kWave) + wave) * kCentPosPerWave;
   if (p0 >= n) return;
-  const int p1 = min(n, p0 + kCentPosPerWave);
-  const int32_t* si = sorted_idx + (size_t)b * n;
-  const int32_t* sl = sorted_labels + (size_t)b * n;
+  const int cnt = min(n - p0, kCentPosPerWave);
+  const int32_t* si = sorted_idx + (size_t)b * n + p0;
+  const int32_t* sl = sorted_labels + (size_t)b * n + p0;
   const uint32_t* xb = x + (size_t)b * n * 64;
   double* sb = sums + (size_t)b * k * 128;
-  int cur = sl[p0];
-  double a0 = 0.0, a1 = 0.0;
-  for (int p = p0; p < p1; p += kCentUnroll) {
-    uint32_t w[kCentUnroll];
-    int lab[kCentUnroll];
+  // The wave's 128 (index, label) pairs in two vector loads; positions past the end read as
+  // index -1 (contributes 0) and the last valid label (no flush).
+  int idx2[2], lab2[2];
 #pragma unroll
-    for (int u = 0; u < kCentUnroll; ++u) {
-      const int q = min(p + u, p1 - 1);
-      lab[u] = sl[q];
-      const int src = si[q];
-      w[u] = ((unsigned)src < (unsigned)n) ? xb[(size_t)src * 64 + lane] : 0u;
+  for (int half = 0; half < 2; ++half) {
+    const int u = half * kWave + lane;
+    idx2[half] = u < cnt ? si[u] : -1;
+    lab2[half] = sl[min(u, cnt - 1)];
+  }
+  auto fetch = [&](uint32_t* w, int base) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kCentBatch; ++u) {
+      const int pos = base + u;  // compile-time after unrolling of the batch loop
+      const int src = __builtin_amdgcn_readlane(idx2[pos / kWave], pos % kWave);
+      // unconditional load (row 0 stands in for an invalid index) so that the loads of a batch
+      // stay counted in order; the value is masked after it arrives
+      const uint32_t v = xb[(size_t)((unsigned)src < (unsigned)n ? src : 0) * 64 + lane];
+      w[u] = ((unsigned)src < (unsigned)n) ? v : 0u;
     }
+  };
+  int cur = __builtin_amdgcn_readlane(lab2[0], 0);
+  double a0 = 0.0, a1 = 0.0;
+  uint32_t wb[2][kCentBatch];
+  fetch(wb[0], 0);
 #pragma unroll
-    for (int u = 0; u < kCentUnroll; ++u) {
-      if (p + u >= p1) break;
-      if (lab[u] != cur) {
+  for (int bt = 0; bt < kCentPosPerWave / kCentBatch; ++bt) {
+    if (bt + 1 < kCentPosPerWave / kCentBatch) fetch(wb[(bt + 1) & 1], (bt + 1) * kCentBatch);
+#pragma unroll
+    for (int u = 0; u < kCentBatch; ++u) {
+      const int pos = bt * kCentBatch + u;
+      const int lab = __builtin_amdgcn_readlane(lab2[pos / kWave], pos % kWave);
+      if (lab != cur) {
         if ((unsigned)cur < (unsigned)k) {
           atomicAdd(&sb[(size_t)cur * 128 + 2 * lane], a0);
           atomicAdd(&sb[(size_t)cur * 128 + 2 * lane + 1], a1);
         }
         a0 = 0.0;
         a1 = 0.0;
-        cur = lab[u];
+        cur = lab;
       }
-      a0 += (double)bf16_to_f32((uint16_t)(w[u] & 0xffffu));
-      a1 += (double)bf16_to_f32((uint16_t)(w[u] >> 16));
+      const uint32_t w = wb[bt & 1][u];
+      a0 += (double)bf16_to_f32((uint16_t)(w & 0xffffu));
+      a1 += (double)bf16_to_f32((uint16_t)(w >> 16));
     }
   }
   if ((unsigned)cur < (unsigned)k) {

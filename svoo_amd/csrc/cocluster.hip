@@ -7,16 +7,15 @@
 //
 // prep:   P = l2norm(bf16(A B^T)) with exact (fp64) dots, E = P B in fp64, split into two bf16
 //         matrices E_hi + E_lo so the bf16 MFMA sees E to ~16 significant bits.
-// assign: 4 waves x 64 tokens per block; token rows stay in registers as the MFMA B operand,
-//         E streams through LDS in 64-row chunks (hi and lo), and each lane keeps a running
-//         argmax over the 16 cluster rows it holds of every 32x32 accumulator tile.
+// assign: 4 waves x 128 tokens per block; token rows stay in registers as the MFMA B operand,
+//         E streams through LDS in 64-row chunks (hi and lo, double buffered, LDS DMA), and each
+//         lane keeps a running argmax over the 16 cluster rows it holds of every 32x32 tile.
 #include "svoo_common.h"
 
 namespace svoo {
 
 constexpr int kPrepMaxLds = 52 * 1024;  // LDS budget of the prep kernel's profile rows
 constexpr int kAssignChunk = 64;   // E rows staged in LDS per step
-constexpr int kLdsRow = 136;       // bf16 elements per staged row (128 + 8 pad)
 
 // --------------------------------------------------------------------------------------- prep
 // kPrepRows rows of A per block: 8 when there are many rows (the key side) and the profile width
@@ -123,64 +122,90 @@ __global__ void __launch_bounds__(256) cocluster_prep_kernel(const uint16_t* __r
 }
 
 // --------------------------------------------------------------------------------------- assign
-__global__ void __launch_bounds__(256) cocluster_assign_kernel(const uint16_t* __restrict__ x,
-                                                               const uint16_t* __restrict__ e_hi,
-                                                               const uint16_t* __restrict__ e_lo,
-                                                               int32_t* __restrict__ labels, int n, int j, int jpad) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_hi[kAssignChunk * kLdsRow];
-  __shared__ __attribute__((aligned(16))) uint16_t s_lo[kAssignChunk * kLdsRow];
+// Block = 4 waves x 128 tokens (4 MFMA column blocks of 32 per wave); the token rows stay in
+// registers as the MFMA B operand for the whole pass.  E_hi and E_lo stream through LDS in chunks
+// of 64 rows, double buffered and filled by LDS DMA (unpadded rows, XOR-swizzled 16-byte chunks),
+// one barrier per chunk.  Each lane keeps a running argmax over the 16 cluster rows it holds of
+// each 32x32 accumulator tile; ties resolve to the lowest cluster index.
+constexpr int kAsgTokWave = 128;
+constexpr int kAsgTok = 4 * kAsgTokWave;
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi,
+                        const uint16_t* __restrict__ e_lo, int32_t* __restrict__ labels, int n, int j, int jpad) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_e[2][2][kAssignChunk * 128];  // [buffer][hi, lo]
   const int bidx = blockIdx.y;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int h = lane / 32, l32 = lane % 32;
-  const int tok0 = blockIdx.x * 256 + wave * 64;
+  const int tok0 = blockIdx.x * kAsgTok + wave * kAsgTokWave;
   const uint16_t* xb = x + (size_t)bidx * n * 128;
   const uint16_t* hb = e_hi + (size_t)bidx * jpad * 128;
   const uint16_t* lb = e_lo + (size_t)bidx * jpad * 128;
+  const int nchunks = jpad / kAssignChunk;
 
-  // Token operands: B[k = d][n = token], lane provides 8 consecutive d of token (l32) per k-step.
-  u32x4_t xop[2][8];
+  // DMA of chunk c into buffer bf: wave w moves rows 16 w .. 16 w + 15 of both matrices, 4 rows
+  // (1 KB) per instruction; lane i fills LDS chunk i%16 of row 4 g + i/16 from its logical chunk.
+  const int prow = lane / 16, pch = lane % 16;
+  auto issue = [&](int c, int bf) __attribute__((always_inline)) {
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
+    for (int g = 0; g < 4; ++g) {
+      const int r = 16 * wave + 4 * g + prow;
+      const size_t src = (size_t)(c * kAssignChunk + r) * 128 + swz(r, pch) * 8;
+      lds_dma16(hb + src, &s_e[bf][0][(16 * wave + 4 * g) * 128]);
+      lds_dma16(lb + src, &s_e[bf][1][(16 * wave + 4 * g) * 128]);
+    }
+  };
+  issue(0, 0);
+
+  // Token operands: B[k = d][n = token], lane provides 8 consecutive d of token l32 per k-step.
+  u32x4_t xop[4][8];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
     const int row = min(tok0 + cb * 32 + l32, n - 1);
     const u32x4_t* src = (const u32x4_t*)(xb + (size_t)row * 128);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) xop[cb][ks] = src[ks * 2 + h];
   }
-
-  float best_v[2] = {-INFINITY, -INFINITY};
-  int best_j[2] = {0, 0};
-
-  for (int jc = 0; jc < jpad; jc += kAssignChunk) {
-    __syncthreads();
+  int aoff[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i;  // 1024 16-byte pieces per matrix
-      const int row = c / 16, part = c % 16;
-      const u32x4_t vh = ((const u32x4_t*)(hb + (size_t)(jc + row) * 128))[part];
-      const u32x4_t vl = ((const u32x4_t*)(lb + (size_t)(jc + row) * 128))[part];
-      *(u32x4_t*)(&s_hi[row * kLdsRow + part * 8]) = vh;
-      *(u32x4_t*)(&s_lo[row * kLdsRow + part * 8]) = vl;
-    }
+  for (int ks = 0; ks < 8; ++ks) aoff[ks] = l32 * 128 + swz(l32, ks * 2 + h) * 8;
+
+  float best_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  int best_j[4] = {0, 0, 0, 0};
+
+  for (int c = 0; c < nchunks; ++c) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if (c + 1 < nchunks) issue(c + 1, (c + 1) & 1);
+    const uint16_t* sh = s_e[c & 1][0];
+    const uint16_t* sl = s_e[c & 1][1];
+    // A operands one k-step ahead of the MFMAs that use them
+    u32x4_t ah = *(const u32x4_t*)(sh + aoff[0]);
+    u32x4_t al = *(const u32x4_t*)(sl + aoff[0]);
 #pragma unroll
     for (int rb = 0; rb < kAssignChunk / 32; ++rb) {
-      f32x16_t acc[2] = {};
+      f32x16_t acc[4] = {};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const int off = (rb * 32 + l32) * kLdsRow + ks * 16 + h * 8;
-        const bf16x8_t ah = as_bf16x8(*(const u32x4_t*)(&s_hi[off]));
-        const bf16x8_t al = as_bf16x8(*(const u32x4_t*)(&s_lo[off]));
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          acc[cb] = mfma32x32x16(ah, as_bf16x8(xop[cb][ks]), acc[cb]);
-          acc[cb] = mfma32x32x16(al, as_bf16x8(xop[cb][ks]), acc[cb]);
+        const u32x4_t ch = ah, cl = al;
+        if (ks < 7 || rb + 1 < kAssignChunk / 32) {
+          const int nrb = ks < 7 ? rb : rb + 1, nks = (ks + 1) % 8;
+          ah = *(const u32x4_t*)(sh + nrb * 32 * 128 + aoff[nks]);
+          al = *(const u32x4_t*)(sl + nrb * 32 * 128 + aoff[nks]);
         }
-      }
+        // keep the next k-step's LDS reads ahead of this step's eight MFMAs
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
+        for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma32x32x16(as_bf16x8(ch), as_bf16x8(xop[cb][ks]), acc[cb]);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma32x32x16(as_bf16x8(cl), as_bf16x8(xop[cb][ks]), acc[cb]);
+      }
+      const int jb = c * kAssignChunk + rb * 32 + h * 4;
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int jj = jc + rb * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+          const int jj = jb + (r / 4) * 8 + (r % 4);
           const float v = acc[cb][r];
           if (jj < j && v > best_v[cb]) {
             best_v[cb] = v;
@@ -191,7 +216,7 @@ __global__ void __launch_bounds__(256) cocluster_assign_kernel(const uint16_t* _
     }
   }
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
+  for (int cb = 0; cb < 4; ++cb) {
     const float ov = __shfl_xor(best_v[cb], 32);
     const int oj = __shfl_xor(best_j[cb], 32);
     if (ov > best_v[cb] || (ov == best_v[cb] && oj < best_j[cb])) {
@@ -237,7 +262,7 @@ static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uin
 
 static int assign_launch(const uint16_t* x, const uint16_t* e_hi, const uint16_t* e_lo, int32_t* labels, int bh, int n,
                          int j, int jpad, hipStream_t stream) {
-  dim3 grid((n + 255) / 256, bh);
+  dim3 grid((n + kAsgTok - 1) / kAsgTok, bh);
   hipLaunchKernelGGL(cocluster_assign_kernel, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad);
   return check_launch("svoo_cocluster_assign");
 }

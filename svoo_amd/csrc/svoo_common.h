@@ -67,6 +67,19 @@ __device__ __forceinline__ uint2 ds_read_tr16_b64(const uint16_t* lds_ptr) {
   return __builtin_bit_cast(uint2, r);
 }
 
+// Physical 16-byte chunk of logical chunk c in row r of an LDS tile of unpadded 256-byte rows.  The
+// XOR pattern makes both read patterns used here conflict-free: 16 consecutive rows at one chunk
+// (MFMA A-operand rows via ds_read_b128) and 4 consecutive rows x 4 consecutive chunks (the
+// transposing reads).
+__device__ __forceinline__ int swz(int r, int c) { return c ^ (((r & 3) << 2) | ((r >> 2) & 3)); }
+
+// Direct global -> LDS copy of 16 bytes per lane: lane i writes lds_base + 16 i (gfx950 LDS DMA,
+// global_load_lds_dwordx4).  lds_base must be wave-uniform; completion is tracked by vmcnt.
+__device__ __forceinline__ void lds_dma16(const void* src, uint16_t* lds_base) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                   (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+
 // ---------------------------------------------------------------- block reductions
 template <int kThreads>
 __device__ __forceinline__ double block_sum_f64(double v, double* scratch) {

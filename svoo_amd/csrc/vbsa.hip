@@ -158,11 +158,6 @@ __device__ __forceinline__ long long xcd_item(long long bid) {
 }
 
 // ------------------------------------------------------------------------------------------ attention
-// Physical 16-byte chunk of logical chunk c in tile row r (rows are 256 bytes, unpadded).  The XOR
-// pattern makes both LDS read patterns conflict-free: 16 consecutive rows at one chunk (the K
-// operand reads) and 4 consecutive rows x 4 consecutive chunks (the transposed V reads).
-__device__ __forceinline__ int swz(int r, int c) { return c ^ (((r & 3) << 2) | ((r >> 2) & 3)); }
-
 // Position cursor over the segmented KV stream: row = off + p while p < next.
 struct KvCursor {
   int seg, off, next;
@@ -191,12 +186,6 @@ __device__ __forceinline__ int cursor_row(KvCursor& c, const int32_t* seg_start,
 //   * O^T += V(t)^T P^T (MFMA, A = V columns via the transposing LDS read, B = the score
 //     accumulators' registers, whose key order the V read follows),
 //   * stores K(t+2) and V(t+1) into the buffers freed by K(t) and V(t-1).
-// Direct global -> LDS copy of 16 bytes per lane: lane i writes lds_base + 16 i (gfx950 LDS DMA).
-__device__ __forceinline__ void lds_dma16(const void* src, uint16_t* lds_base) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                   (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
-}
-
 // Ping-pong block: 8 waves in two groups of 4 (group A = waves 0-3, group B = waves 4-7), each
 // wave 32 queries (query tile 256: A owns queries 0-127, B 128-255).  The waves of a SIMD come
 // from different groups and alternate between an MFMA phase M(t) = {O += V(t)^T P(t)^T, S(t+1) =
