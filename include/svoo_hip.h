@@ -90,9 +90,10 @@ int svoo_l2norm_rows(const void* x, int x_is_bf16, float* y, long long rows, int
 /* ---------------------------------------------------------------------------------------------
  * Co-clustering (profile-space k-means).
  *   svoo_cocluster_prep: P = l2norm(bf16(A B^T)) ([BH][J][KP], optional output), E = P B split into
- *     E_hi = bf16(E), E_lo = bf16(E - E_hi), both [BH][jpad][D] with zero rows J..jpad-1.
+ *     E_hi = bf16(E), E_lo = bf16(E - E_hi), both [BH][jpad][D]; rows J..jpad-1 repeat row J-1.
  *     Replaces torch.matmul + triton_l2norm_forward, svoo/co_clustering.py:2427-2428,2440-2441.
- *   svoo_cocluster_assign: labels[b][n] = argmax_j x[b][n] . (E_hi + E_lo)[b][j]  (first j on ties);
+ *   svoo_cocluster_assign: labels[b][n] = argmax_j x[b][n] . (E_hi + E_lo)[b][j]  (first j on ties),
+ *     with E_hi / E_lo as svoo_cocluster_prep writes them (padding rows repeating row J-1);
  *     equal to argmin_j 2 - 2 (x C^T / ||x C^T||) . P_j of profile_norm_triton + fused_cocluster_assign_triton,
  *     svoo/co_clustering.py:2086-2400, because ||x C^T|| > 0 is a per-token constant.
  *   svoo_co_cluster: max_iters x (key step, query step), all on device, no host synchronisation.

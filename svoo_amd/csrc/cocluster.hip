@@ -34,11 +34,14 @@ __global__ void __launch_bounds__(256) cocluster_prep_kernel(const uint16_t* __r
   const int tid = threadIdx.x;
   const uint16_t* ab = a + (size_t)bidx * j * 128;
   const uint16_t* bb = bmat + (size_t)bidx * kp * 128;
-  const int nrows = max(0, min(kPrepRows, j - r0));
+  // Rows r0 .. r0 + nrows - 1 are computed; padding rows (j <= row < jpad) repeat row j - 1, so
+  // that a padding row can only tie with row j - 1 in the assignment's argmax.
+  const int nrows = max(0, min(kPrepRows, jpad - r0));
+  const int nreal = max(0, min(kPrepRows, j - r0));
 
   for (int t = tid; t < kPrepRows * 128; t += 256) {
     const int r = t / 128, dd = t % 128;
-    arow[t] = (r < nrows) ? (double)bf16_to_f32(ab[(size_t)(r0 + r) * 128 + dd]) : 0.0;
+    arow[t] = (r < nrows) ? (double)bf16_to_f32(ab[(size_t)min(r0 + r, j - 1) * 128 + dd]) : 0.0;
   }
   __syncthreads();
 
@@ -85,7 +88,7 @@ __global__ void __launch_bounds__(256) cocluster_prep_kernel(const uint16_t* __r
 
   if (profile) {
     float* pb = profile + (size_t)bidx * j * kp;
-    for (int t = tid; t < nrows * kp; t += 256) {
+    for (int t = tid; t < nreal * kp; t += 256) {
       const int r = t / kp, k = t % kp;
       pb[(size_t)(r0 + r) * kp + k] = (float)((double)praw[r * kp + k] * inv[r]);
     }
@@ -166,9 +169,11 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) xop[cb][ks] = src[ks * 2 + h];
   }
-  int aoff[8];
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) aoff[ks] = l32 * 128 + swz(l32, ks * 2 + h) * 8;
+  // LDS element offset of A-operand k-step ks in row l32: swz(l32, 2 ks + h) * 8, written as
+  // 16 (ks ^ g) + 8 e so that it costs one xor per use instead of eight live registers.
+  const int sw = swz(l32, 0), g = sw >> 1;
+  const int abase = l32 * 128 + 8 * (h ^ (sw & 1));
+#define AOFF(ks) (abase + 16 * ((ks) ^ g))
 
   float best_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   int best_j[4] = {0, 0, 0, 0};
@@ -180,8 +185,8 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
     const uint16_t* sh = s_e[c & 1][0];
     const uint16_t* sl = s_e[c & 1][1];
     // A operands one k-step ahead of the MFMAs that use them
-    u32x4_t ah = *(const u32x4_t*)(sh + aoff[0]);
-    u32x4_t al = *(const u32x4_t*)(sl + aoff[0]);
+    u32x4_t ah = *(const u32x4_t*)(sh + AOFF(0));
+    u32x4_t al = *(const u32x4_t*)(sl + AOFF(0));
 #pragma unroll
     for (int rb = 0; rb < kAssignChunk / 32; ++rb) {
       f32x16_t acc[4] = {};
@@ -190,8 +195,8 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
         const u32x4_t ch = ah, cl = al;
         if (ks < 7 || rb + 1 < kAssignChunk / 32) {
           const int nrb = ks < 7 ? rb : rb + 1, nks = (ks + 1) % 8;
-          ah = *(const u32x4_t*)(sh + nrb * 32 * 128 + aoff[nks]);
-          al = *(const u32x4_t*)(sl + nrb * 32 * 128 + aoff[nks]);
+          ah = *(const u32x4_t*)(sh + nrb * 32 * 128 + AOFF(nks));
+          al = *(const u32x4_t*)(sl + nrb * 32 * 128 + AOFF(nks));
         }
         // keep the next k-step's LDS reads ahead of this step's eight MFMAs
         __builtin_amdgcn_sched_barrier(0);
@@ -200,21 +205,24 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma32x32x16(as_bf16x8(cl), as_bf16x8(xop[cb][ks]), acc[cb]);
       }
-      const int jb = c * kAssignChunk + rb * 32 + h * 4;
+      // Row of element r is jb + (r/4)*8 + r%4 + 4h; the lane term 4h is added once at the end,
+      // so the selected index is a wave-uniform constant.
+      const int jb = c * kAssignChunk + rb * 32;
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int jj = jb + (r / 4) * 8 + (r % 4);
           const float v = acc[cb][r];
-          if (jj < j && v > best_v[cb]) {
-            best_v[cb] = v;
-            best_j[cb] = jj;
-          }
+          const bool up = v > best_v[cb];
+          best_v[cb] = fmaxf(v, best_v[cb]);
+          best_j[cb] = up ? jb + (r / 4) * 8 + (r % 4) : best_j[cb];
         }
       }
     }
   }
+#undef AOFF
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) best_j[cb] += h * 4;
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
     const float ov = __shfl_xor(best_v[cb], 32);
@@ -224,7 +232,8 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
       best_j[cb] = oj;
     }
     const int tok = tok0 + cb * 32 + l32;
-    if (h == 0 && tok < n) labels[(size_t)bidx * n + tok] = best_j[cb];
+    // padding rows repeat row j - 1: a padding winner stands for row j - 1
+    if (h == 0 && tok < n) labels[(size_t)bidx * n + tok] = min(best_j[cb], j - 1);
   }
 }
 
