@@ -47,6 +47,8 @@ def parse_args():
                     help="C2-C4: one SVOO attention call; C5: one denoising step of a random-init Wan2.1-1.3B DiT")
     ap.add_argument("--mode", default="density", choices=["density", "reference"],
                     help="density: top_p=0, min_kc_ratio=rho_h; reference: top_p=0.9, min_kc_ratio=clip(rho_h,0.15,0.2)")
+    ap.add_argument("--sparsity-profile", action="store_true",
+                    help="time the offline profile producer (exact per-head sparsity of one layer) instead")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU baseline sample")
@@ -77,6 +79,8 @@ def main():
 
     if args.config == "C5":
         return main_dit(args)
+    if args.sparsity_profile:
+        return main_profile(args)
 
     import numpy as np
     import torch
@@ -439,6 +443,106 @@ def main_dit(args):
         "svoo_calls_ms": round(svoo_ms, 3),
         "stages_ms": {kk: round(vv, 3) for kk, vv in stages_ms.items()},
         "realized_density": round(density, 5),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def main_profile(args):
+    """Offline profile producer on one layer of the chosen config (default inputs of C2/C3/C4): exact
+    per-head sparsity (threshold 0.95, every query row) with ``compute_exact_attention_sparsity``.
+    Timed: the whole call, and inside it the score GEMMs and the HIP count kernel separately; beside
+    it, the reference's own formulation (fp32 softmax, sort, cumsum, searchsorted) on the same GPU
+    and inputs for a sample of rows, and the numpy oracle on the host for a sample of rows."""
+    import numpy as np
+    import torch
+
+    from svoo_amd import _lib, synth
+    from svoo_amd.sparsity import compute_exact_attention_sparsity, exact_counts_from_scores
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a HIP device")
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    cfg = synth.CONFIGS[args.config]
+    h, n, d = cfg.heads, cfg.tokens, cfg.head_dim
+    q, k, _ = synth.make_qkv_device(cfg, dev)
+    torch.cuda.synchronize()
+    thr = 0.95
+    scale = d ** -0.5
+    # warm-up on a slice, then the timed full call
+    compute_exact_attention_sparsity(q[:, :, :256], k, threshold=thr)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    avg, per_head, stats = compute_exact_attention_sparsity(q, k, threshold=thr)
+    e1.record()
+    torch.cuda.synchronize()
+    t_call = e0.elapsed_time(e1)
+    chunk = stats["chunk_size"]
+    log(f"profile producer {cfg.name}: {t_call:.1f} ms per layer (chunk {chunk} rows), avg sparsity {avg:.4f}")
+
+    # split: GEMM and count kernel on one chunk, scaled by the number of chunks
+    rows = min(chunk, n)
+    kt = k.transpose(-2, -1)
+    g0, g1, c1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    g0.record()
+    sc = torch.matmul(q[:, :, :rows], kt)
+    g1.record()
+    exact_counts_from_scores(sc, scale, thr)
+    c1.record()
+    torch.cuda.synchronize()
+    nchunks = (n + rows - 1) // rows
+    t_gemm = g0.elapsed_time(g1) * n / rows
+    t_count = g1.elapsed_time(c1) * n / rows
+    count_bytes = 3 * 2.0 * h * rows * n  # three passes over bf16 scores
+    count_gbps = count_bytes / (g1.elapsed_time(c1) * 1e-3) / 1e9
+
+    # the reference formulation on the same GPU for a sample of rows (fp32 probabilities, sort, cumsum)
+    sample = min(512, n)
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record()
+    w = torch.softmax(torch.matmul(q[:, :, :sample], kt).float() * scale, dim=-1)
+    cs = torch.cumsum(torch.sort(w, dim=-1, descending=True).values, dim=-1)
+    ref_counts = torch.searchsorted(cs, (thr * cs[..., -1:]).contiguous(), right=False, out_int32=True).squeeze(-1) + 1
+    r1.record()
+    torch.cuda.synchronize()
+    t_ref = r0.elapsed_time(r1) * n / sample
+    mine = exact_counts_from_scores(torch.matmul(q[:, :, :sample], kt), scale, thr)
+    agree = float((mine == ref_counts).float().mean().item())
+    maxdiff = int((mine - ref_counts).abs().max().item())
+    del w, cs
+    log(f"reference formulation on the GPU: {t_ref:.1f} ms per layer (from {sample} rows); counts agree on "
+        f"{agree * 100:.2f}% of rows, max difference {maxdiff}")
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import svoo_oracle as O
+
+        rows_cpu = 8
+        s_cpu = torch.matmul(q[:, :1, :rows_cpu], kt[:, :1]).float().cpu().numpy()
+        t0 = time.perf_counter()
+        O.exact_sparsity_counts(s_cpu, scale, thr)
+        t_host = time.perf_counter() - t0
+        per_layer_s = t_host * h * n / rows_cpu
+        cpu = {"value": round(per_layer_s * 1e3, 1), "unit": "ms per layer", "cores": cpu_threads(), "kind": "port",
+               "sample": f"{rows_cpu} query rows of 1 head (scores from the GPU GEMM) through the numpy oracle's "
+                         f"sort/cumsum count: {t_host:.3f} s, scaled x{h * n // rows_cpu} to {per_layer_s:.1f} s"}
+
+    line = {
+        "metric": "exact per-head attention sparsity of one layer (offline profile producer), ms, 1 GPU",
+        "value": round(t_call, 3),
+        "unit": "ms per layer (all query rows, threshold 0.95)",
+        "n_gpus": 1, "steps": 1, "warmup": 1, "ms_per_step": round(t_call, 3), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded Gaussian mixture with per-frame drift, drawn on device)",
+        "config": {"workload": f"{cfg.name}: exact sparsity profile of one layer, H={h} Sq=Sk={n} d={d}",
+                   "heads": h, "tokens": n, "threshold": thr, "chunk_rows": chunk},
+        "gemm_ms": round(t_gemm, 3), "count_kernel_ms": round(t_count, 3),
+        "count_kernel_gbps": round(count_gbps, 1), "count_kernel_frac_hbm": round(count_gbps / HBM_PEAK_GBPS, 4),
+        "reference_formulation_ms": round(t_ref, 3), "speedup_vs_reference_formulation": round(t_ref / t_call, 2),
+        "counts_agree_with_reference_formulation": round(agree, 5),
+        "avg_sparsity": round(avg, 6),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

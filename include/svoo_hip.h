@@ -150,6 +150,18 @@ int svoo_vbsa_segments(const uint8_t* map, const int32_t* k_sizes, int bh, int q
                        int32_t* seg_len, int32_t* seg_count, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Offline profile producer: exact attention sparsity.
+ *   svoo_exact_sparsity_counts: for each of `rows` rows of n bf16 attention scores, the smallest
+ *   number of keys whose softmax weights (of scores * scale) hold `threshold` of the row's mass;
+ *   counts int32 [rows].  Weights are float(exp(double(s - max))) with s = float(score) * scale in
+ *   fp32; masses are fp64 sums in descending order.  Replaces the sort / cumsum / searchsorted of
+ *   _exact_counts_from_scores and counts_from_sorted_probabilities_triton
+ *   (svoo/sparsity/exact.py:110-155, svoo/kernels/triton/sparsity.py:9-106).
+ * ------------------------------------------------------------------------------------------- */
+int svoo_exact_sparsity_counts(const uint16_t* scores, long long rows, int n, float scale, float threshold,
+                               int32_t* counts, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Diagnostic (no reference counterpart): runs one v_mfma_f32_32x32x16_bf16 and one
  * v_mfma_f32_16x16x32_bf16 on index-coded operands and writes the raw per-lane accumulators
  * (out32: 64 lanes x 16 floats, out16: 64 lanes x 4 floats), so tests can confirm the operand

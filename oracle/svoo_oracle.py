@@ -49,6 +49,9 @@ __all__ = [
     "hunyuan_post_process",
     "hunyuan_attention_call",
     "hunyuan_dense_attention",
+    "sparsity_weights",
+    "exact_sparsity_counts",
+    "exact_attention_sparsity",
 ]
 
 _FIX_SHIFT = 60  # fixed-point scale of the top-p prefix sums (2**60)
@@ -691,3 +694,49 @@ def hunyuan_dense_attention(query, key, value, valid_length: int, compute_dtype=
     m[:, :, 0, 0] = m[:, :, 1, 1] = True
     sz = np.broadcast_to(np.array([valid_length, s - valid_length]), (b, h, 2))
     return block_sparse_attention(query, key, value, m, sz, sz, compute_dtype)
+
+
+# --------------------------------------------------------------------------------------
+# Offline profile producer: exact attention sparsity
+# --------------------------------------------------------------------------------------
+def sparsity_weights(scores, scale: float) -> np.ndarray:
+    """Unnormalised softmax weights of score rows: ``float32(exp(float64(s - m)))`` with
+    ``s = float32(score) * float32(scale)`` and ``m`` the row max (fp32 subtraction).  The reference
+    softmaxes ``matmul(q, k^T).float() * scale`` (``svoo/sparsity/exact.py:216-221``); counts depend
+    only on ratios of weights, so the normalisation by the row sum is left out."""
+    s = np.asarray(scores, dtype=np.float32) * np.float32(scale)
+    m = s.max(axis=-1, keepdims=True)
+    return np.exp((s - m).astype(np.float64)).astype(np.float32)
+
+
+def exact_sparsity_counts(scores, scale: float, threshold: float) -> np.ndarray:
+    """Per-row key count covering ``threshold`` of the mass: weights sorted descending, fp64 cumulative
+    sum, ``searchsorted(cumsum, threshold * total, right=False) + 1``
+    (``svoo/sparsity/exact.py:110-155``, in fp64 where the reference's cumsum is fp32)."""
+    e = sparsity_weights(scores, scale).astype(np.float64)
+    w = -np.sort(-e, axis=-1)
+    cum = np.cumsum(w, axis=-1)
+    target = threshold * cum[..., -1:]
+    return (cum < target).sum(axis=-1).astype(np.int64) + 1
+
+
+def exact_attention_sparsity(query, key, threshold: float = 0.95, query_sample_size: int = 0):
+    """``compute_exact_attention_sparsity`` (``svoo/sparsity/exact.py:177-246``): bf16 scores
+    ``bf16(q . k)`` (exact dots rounded like a bf16 matmul output), per-row counts, per-head mean of
+    ``count / Sk``.  Returns ``(avg, per_head, counts)``; query rows are sampled as the reference
+    does (uniform ``linspace`` positions, rounded, duplicates dropped)."""
+    q = np.asarray(query, dtype=np.float32)
+    k = np.asarray(key, dtype=np.float32)
+    b, h, sq, d = q.shape
+    sk = k.shape[2]
+    if query_sample_size and 0 < query_sample_size < sq:
+        if query_sample_size == 1:
+            pos = np.array([sq // 2])
+        else:
+            # torch.linspace in float32, then round-half-even and unique_consecutive
+            pos = np.unique(np.round(np.linspace(0, sq - 1, query_sample_size, dtype=np.float32)).astype(np.int64))
+        q = q[:, :, pos]
+    scores = bf16_round(np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k.astype(np.float64)).astype(np.float32))
+    counts = exact_sparsity_counts(scores, d ** -0.5, threshold)
+    per_head = (counts / float(sk)).mean(axis=(0, 2))
+    return float(per_head.mean()), per_head.tolist(), counts

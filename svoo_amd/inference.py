@@ -11,6 +11,8 @@ No kernel warm-up is needed: the HIP kernels are compiled ahead of time.
 
 from __future__ import annotations
 
+import os
+
 from .processor import WanAttn_SAPAttn_Processor
 from .sparsity import SparsityLookup
 
@@ -51,6 +53,12 @@ def replace_wan_attention(
     sparsity_csv_path=None,
     dynamic_min_kc_ratio_min=None,
     dynamic_min_kc_ratio_max=None,
+    measure_attention_sparsity=False,
+    sparsity_output_file="attention_sparsity.txt",
+    sparsity_batch_size=0,
+    sparsity_query_samples=0,
+    sparsity_threshold=0.95,
+    sparsity_start_step=1,
     processor_cls=WanAttn_SAPAttn_Processor,
     **unused,
 ):
@@ -61,7 +69,9 @@ def replace_wan_attention(
     passes them.  ``max_kc_ratio`` is forwarded to the mask.  Only the SVOO ``"SAP"`` pattern is
     built here: other patterns raise ``ValueError`` as the reference does for unsupported ones, and
     the EAR / global-constraint / routing variants raise ``NotImplementedError``.  A missing or
-    unreadable profile CSV disables the dynamic ratios (``:308-320``).  Returns the processors.
+    unreadable profile CSV disables the dynamic ratios (``:308-320``).  With
+    ``measure_attention_sparsity`` every processor also appends the exact per-head sparsity of each
+    (layer, step) to ``sparsity_output_file`` (the offline profile producer).  Returns the processors.
     """
     if pattern != "SAP" or not use_svoo:
         raise ValueError("Only the SVOO SAP pattern is supported by this build (pattern='SAP', use_svoo=True).")
@@ -104,6 +114,20 @@ def replace_wan_attention(
         except Exception:  # the reference silently falls back to the scalar ratio
             cls.use_dynamic_min_kc_ratio = False
             cls.sparsity_lookup = None
+
+    # offline profiling (inference.py:322-341): a fresh raw log unless SVOO_SPARSITY_RESUME keeps it
+    cls.measure_attention_sparsity = measure_attention_sparsity
+    cls.sparsity_output_file = sparsity_output_file
+    cls.sparsity_batch_size = sparsity_batch_size
+    cls.sparsity_query_samples = sparsity_query_samples
+    cls.sparsity_threshold = sparsity_threshold
+    cls.sparsity_start_step = sparsity_start_step
+    if measure_attention_sparsity and sparsity_output_file:
+        d = os.path.dirname(sparsity_output_file)
+        if d:
+            os.makedirs(d, exist_ok=True)
+        if os.environ.get("SVOO_SPARSITY_RESUME", "0") in ("0", "", "false", "False"):
+            open(sparsity_output_file, "w", encoding="utf-8").close()
 
     processors = []
     for transformer in (pipe.transformer, getattr(pipe, "transformer_2", None)):

@@ -24,6 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from .co_clustering import block_mask_lengths, co_cluster_tokens_full, dynamic_block_sparse_fwd
+from .sparsity.exact import compute_exact_attention_sparsity, format_sparsity_log, has_completed_sparsity_entry
 from .permute import apply_inverse_permutation, apply_inverse_permutation_bshd, permute_pair_by_indices
 from . import _lib
 
@@ -90,7 +91,14 @@ class WanAttn_SAPAttn_Processor:
     use_global_constraints = False
     use_routing_transformer_strategy = False
     enable_mem_save = bool(int(os.environ.get("SVOO_ENABLE_MEM_SAVE", "1")))
+    # Offline profiling: exact per-head sparsity of self-attention, appended to a raw log
+    # (svoo/models/wan/attention.py:395-489); merged into the profile CSV by sparsity.merge.
     measure_attention_sparsity = False
+    sparsity_output_file = None
+    sparsity_batch_size = 0
+    sparsity_query_samples = 0
+    sparsity_threshold = 0.95
+    sparsity_start_step = 1
 
     # Inference-step tracking shared by all instances (svoo/models/wan/attention.py:84-86).
     _current_internal_timestep = None
@@ -107,6 +115,7 @@ class WanAttn_SAPAttn_Processor:
         # When set to a list, the sparse path appends (stage name, recorded torch.cuda.Event) at each
         # stage boundary on the current stream: start, cluster, permute, mask, attention, unpermute.
         self.stage_events = None
+        self._last_logged_step = None
 
     def _mark(self, name: str) -> None:
         if self.stage_events is not None:
@@ -182,6 +191,8 @@ class WanAttn_SAPAttn_Processor:
             hidden_states = F.scaled_dot_product_attention(query, key, value, attn_mask=attention_mask,
                                                            dropout_p=0.0, is_causal=False)
         else:
+            if self.measure_attention_sparsity:
+                self.log_attention_sparsity(query, key, value, timestep, "self")
             hidden_states = self.attention_core_logic(query, key, value, timestep)
         return self.get_o(attn, query, hidden_states, hidden_states_img)
 
@@ -198,6 +209,39 @@ class WanAttn_SAPAttn_Processor:
             cls._inference_step_counter += 1
             cls._current_internal_timestep = internal_t
         return cls._inference_step_counter
+
+    @torch.no_grad()
+    def compute_attention_sparsity(self, query, key, value, attn_type="self", batch_size=0, threshold=0.95,
+                                   query_sample_size=0):
+        """Exact per-head sparsity of this call's attention (``svoo/models/wan/attention.py:395-417``)."""
+        return compute_exact_attention_sparsity(query, key, batch_size=batch_size, threshold=threshold,
+                                                query_sample_size=query_sample_size)
+
+    def log_attention_sparsity(self, query, key, value, timestep, attn_type="self"):
+        """Measure once per (layer, step) from ``sparsity_start_step`` on and append the raw log lines
+        (``svoo/models/wan/attention.py:446-489``); completed entries are skipped on resume."""
+        if not self.measure_attention_sparsity:
+            return
+        step = self._get_inference_step(timestep)
+        if step is None or step < self.sparsity_start_step or self._last_logged_step == step:
+            return
+        self._last_logged_step = step
+        out = self.sparsity_output_file
+        if has_completed_sparsity_entry(out, self.layer_idx, step, query.size(1)):
+            return
+        avg, per_head, stats = self.compute_attention_sparsity(
+            query, key, value, attn_type, batch_size=self.sparsity_batch_size, threshold=self.sparsity_threshold,
+            query_sample_size=self.sparsity_query_samples)
+        lines = format_sparsity_log(self.layer_idx, attn_type, step, self.sparsity_threshold, avg, per_head,
+                                    stats["seq_len"], stats["sampled_seq_len"])
+        for line in lines:
+            print(line)
+        if out:
+            d = os.path.dirname(out)
+            if d:
+                os.makedirs(d, exist_ok=True)
+            with open(out, "a") as f:
+                f.write("\n".join(lines) + "\n")
 
     def flash_attention(self, query, key, value):
         """Dense attention of the full-precision gate (``svoo/models/wan/attention.py:329-331``)."""

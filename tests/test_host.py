@@ -237,3 +237,61 @@ def test_tiny_dit_dense_forward_shapes():
     assert cos.shape == (1, 72, 1, 128)
     # pairs share one angle; the t-axis channels of token 0 (position 0) do not rotate
     assert torch.equal(cos[..., 0::2], cos[..., 1::2]) and torch.all(cos[0, 0, 0] == 1)
+
+
+def test_sparsity_log_merge_roundtrip(tmp_path):
+    from svoo_amd.sparsity import SparsityLookup, format_sparsity_log, merge_sparsity_data, parse_sparsity_file, save_to_csv
+
+    a, b = tmp_path / "run_a.txt", tmp_path / "run_b.txt"
+    with open(a, "w") as f:
+        f.write("\n".join(format_sparsity_log(0, "self", 1, 0.95, 0.2, [0.1, 0.3], 100, 100)) + "\n")
+        f.write("\n".join(format_sparsity_log(1, "self", 1, 0.95, 0.5, [0.5, 0.5], 100, 10)) + "\n")
+    with open(b, "w") as f:
+        f.write("\n".join(format_sparsity_log(0, "self", 1, 0.95, 0.25, [0.2, 0.3], 100, 100)) + "\n")
+    pa = parse_sparsity_file(a)
+    assert pa[(1, 0, 0)] == 0.1 and pa[(1, 1, 1)] == 0.5 and len(pa) == 4
+    merged = merge_sparsity_data([a, b, tmp_path / "missing.txt"])
+    assert merged[(1, 0, 0)] == 0.2 and merged[(1, 0, 1)] == 0.3  # maximum over the runs
+    out = tmp_path / "profile.csv"
+    save_to_csv(merged, out)
+    lk = SparsityLookup(str(out), verbose=False)
+    assert lk.get_sparsity(1, 0, 0) == 0.2 and lk.get_sparsity_batch(1, 1, 2) == [0.5, 0.5]
+    assert open(out).readline().strip() == "Step,Layer,Head,Sparsity"
+
+
+def test_sparsity_resume_guard(tmp_path, monkeypatch):
+    from svoo_amd.sparsity import format_sparsity_log, has_completed_sparsity_entry
+
+    log = tmp_path / "raw.txt"
+    log.write_text("\n".join(format_sparsity_log(3, "self", 7, 0.95, 0.1, [0.1] * 4, 50, 50)) + "\n")
+    monkeypatch.delenv("SVOO_SPARSITY_RESUME", raising=False)
+    assert not has_completed_sparsity_entry(str(log), 3, 7, 4)  # opt-in only
+    monkeypatch.setenv("SVOO_SPARSITY_RESUME", "1")
+    assert has_completed_sparsity_entry(str(log), 3, 7, 4)
+    assert not has_completed_sparsity_entry(str(log), 3, 7, 5)
+    assert not has_completed_sparsity_entry(str(log), 3, 8, 4)
+    with open(log, "a") as f:  # appended entries are picked up incrementally
+        f.write("\n".join(format_sparsity_log(3, "self", 8, 0.95, 0.1, [0.1] * 4, 50, 50)) + "\n")
+    assert has_completed_sparsity_entry(str(log), 3, 8, 4)
+
+
+def test_sparsity_query_sampling_positions():
+    from svoo_amd.sparsity.exact import _sample_query_rows
+
+    q = torch.arange(64, dtype=torch.float32).view(1, 1, 64, 1)
+    sub, n = _sample_query_rows(q, 5)
+    assert n == 5 and sub.flatten().tolist() == [0, 16, 32, 47, 63]
+    assert _sample_query_rows(q, 1)[0].flatten().tolist() == [32]
+    assert _sample_query_rows(q, 0)[1] == 64 and _sample_query_rows(q, 99)[1] == 64
+
+
+def test_exact_sparsity_rejects_bad_inputs():
+    from svoo_amd.sparsity import compute_exact_attention_sparsity
+
+    q = torch.zeros(1, 1, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        compute_exact_attention_sparsity(q, q, threshold=1.5)
+    with pytest.raises(ValueError):
+        compute_exact_attention_sparsity(q.float(), q.float())
+    with pytest.raises(ValueError):  # no CPU fallback: the counts run on the HIP device only
+        compute_exact_attention_sparsity(q, q)

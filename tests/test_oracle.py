@@ -299,3 +299,70 @@ def test_hunyuan_call_with_all_blocks_is_dense_varlen():
     init_k = RNG.integers(0, vl, size=(h, 6))
     out = O.hunyuan_attention_call(q, k, v, 4, 6, 2, 1.0, 0, prompt, ctx, init_q_idx=init_q, init_k_idx=init_k)
     np.testing.assert_allclose(out, O.hunyuan_dense_attention(q, k, v, vl + prompt), rtol=1e-9, atol=1e-12)
+
+
+# ---------------------------------------------------------------- exact sparsity (profile producer)
+def _torch_reference_counts(scores, scale, threshold):
+    """The reference's fp32 formulation (svoo/sparsity/exact.py:110-155) restated in torch on the CPU:
+    softmax, descending sort, cumsum, searchsorted(right=False) + 1."""
+    import torch
+
+    t = torch.from_numpy(np.asarray(scores, np.float32)) * scale
+    w = torch.softmax(t, dim=-1)
+    cs = torch.cumsum(torch.sort(w, dim=-1, descending=True).values, dim=-1)
+    target = (threshold * cs[..., -1:]).contiguous()
+    return (torch.searchsorted(cs, target, right=False, out_int32=True).squeeze(-1) + 1).numpy()
+
+
+def test_exact_sparsity_closed_forms():
+    # equal scores: every weight is 1, so c keys hold c/n of the mass -> ceil(threshold * n)
+    for n in (1, 7, 100, 4096):
+        for thr in (0.5, 0.9, 0.95, 1.0):
+            c = O.exact_sparsity_counts(np.zeros((3, n), np.float32), 0.088, thr)
+            assert (c == int(np.ceil(thr * n - 1e-12))).all(), (n, thr, c)
+    # one dominant key holds almost all of the mass
+    s = np.full((2, 1000), -60.0, np.float32)
+    s[:, 123] = 60.0
+    assert (O.exact_sparsity_counts(s, 1.0, 0.95) == 1).all()
+    # two keys of equal weight above a negligible tail: 0.6 of the mass needs both
+    s = np.full((1, 50), -200.0, np.float32)
+    s[0, [3, 9]] = 0.0
+    assert O.exact_sparsity_counts(s, 1.0, 0.6)[0] == 2
+    assert O.exact_sparsity_counts(s, 1.0, 0.5)[0] == 1
+    # threshold 1: exactly the keys whose fp32 weight is non-zero (exp(-120) underflows)
+    s = np.zeros((1, 10), np.float32)
+    s[0, :4] = -120.0
+    assert O.exact_sparsity_counts(s, 1.0, 1.0)[0] == 6
+
+
+def test_exact_sparsity_matches_reference_formulation_and_brute_force():
+    import math
+
+    rng = np.random.default_rng(7)
+    for scale_in, n in ((3.0, 3000), (0.5, 777), (8.0, 256)):
+        sc = O.bf16_round((rng.standard_normal((48, n)) * scale_in).astype(np.float32))
+        mine = O.exact_sparsity_counts(sc, 0.0884, 0.95)
+        ref = _torch_reference_counts(sc, 0.0884, 0.95)
+        # fp32 softmax/cumsum in the reference can move a count by one key at a rounding boundary
+        assert np.abs(mine - ref).max() <= 1 and (mine == ref).mean() >= 0.97
+    # brute force with exact (fsum) prefix sums on small rows
+    sc = O.bf16_round((rng.standard_normal((6, 40)) * 4).astype(np.float32))
+    w = O.sparsity_weights(sc, 0.5)
+    for r in range(6):
+        vals = sorted((float(x) for x in w[r]), reverse=True)
+        tot = math.fsum(vals)
+        c = next(i + 1 for i in range(len(vals)) if math.fsum(vals[: i + 1]) >= 0.9 * tot)
+        assert O.exact_sparsity_counts(sc[r : r + 1], 0.5, 0.9)[0] == c
+
+
+def test_exact_attention_sparsity_per_head_mean():
+    rng = np.random.default_rng(3)
+    q = O.bf16_round(rng.standard_normal((1, 2, 64, 128)).astype(np.float32))
+    k = O.bf16_round(rng.standard_normal((1, 2, 96, 128)).astype(np.float32))
+    avg, per_head, counts = O.exact_attention_sparsity(q, k, 0.9)
+    assert counts.shape == (1, 2, 64)
+    assert np.allclose(per_head, counts[0].mean(axis=1) / 96.0) and abs(avg - np.mean(per_head)) < 1e-12
+    # sampled rows: linspace positions of the sampled query rows only
+    _, _, c5 = O.exact_attention_sparsity(q, k, 0.9, query_sample_size=5)
+    pos = [0, 16, 32, 47, 63]
+    assert np.array_equal(c5, counts[:, :, pos])
