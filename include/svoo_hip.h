@@ -150,6 +150,51 @@ int svoo_vbsa_segments(const uint8_t* map, const int32_t* k_sizes, int bh, int q
                        int32_t* seg_len, int32_t* seg_count, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * EAR (error-aware routing with centroid compensation).  All token inputs are cluster-contiguous
+ * (permuted); k_offsets [BH][KN] is the exclusive prefix of k_sizes.
+ *   svoo_ear_value_stats: per key cluster j the value centroid v_cent[b][j] (compute_vc != 0:
+ *     bf16(bf16(exact member sum) / bf16(max(|K_j|, 1))), an empty cluster gives 0; compute_vc == 0
+ *     reads it), vc_sq[b][j] = |v_cent|^2 (fp32) and, with u_t = v_t - v_cent_j, tok_stats[b][t] =
+ *     {|u_t|^2, u_t . v_cent_j} (fp32 pairs, [BH][N][2]; the reference keeps |v_t|^2 and v_cent_j . v_t,
+ *     from which these follow).  Replaces _compute_value_centroids (svoo/models/wan/attention.py:593-610)
+ *     and _precompute_v_stats_kernel (svoo/co_clustering.py:1315-1396).
+ *   svoo_ear_centroid_logits: c[b][i][j] = bf16(bf16(qc_i . kc_j) * D^-0.5), exact dot.
+ *     Replaces the einsum of svoo/co_clustering.py:1725.
+ *   svoo_ear_efficiency: eff[b][i][j] = log(max(err_ij, eps)) - gamma log(max(|Q_i||K_j|, eps)) with
+ *     err_ij = sum_t || e^{a_t} v_t - e^{c_ij} vc_j ||^2 over the tokens of key cluster j,
+ *     a_t = qc_i . k_t / sqrt(D) (fp32 MFMA), evaluated with the exponents shifted by
+ *     max(c_ij, max_t a_t) and in the centroid-difference form that avoids the cancellation of the
+ *     reference's expansion (fp32 [BH][QN][KN]).  Replaces error_estimation_triton +
+ *     _error_estimation_kernel, svoo/co_clustering.py:1399-1689.
+ *   svoo_ear_select: the EAR block map (uint8 [B][H][QN][KN]) from c and eff: budget = area of the
+ *     top-p prefix (at least budget_preserve[h]) of the bf16 softmax of c + bf16(log(|K| + 1e-8)),
+ *     stably sorted; the first preserve[h] budget-ordered clusters are kept; the others are taken in
+ *     descending efficiency (stable) while the area before them is below the remaining budget.  Areas
+ *     are exact int64.  Replaces the selection of identify_dynamic_map_estimated,
+ *     svoo/co_clustering.py:1692-1797.
+ *   svoo_vbsa_ear_fwd: for each (b, i), softmax attention of Q_i over the tokens of the active key
+ *     clusters and the (k_cent_j, v_cent_j) pairs of the inactive ones, scored
+ *     q . k_cent_j / sqrt(D) + log(|K_j| + 1e-6): one online softmax (fp32, bf16 MFMA).  Workspace and
+ *     status as svoo_vbsa_fwd.  Replaces dynamic_block_sparse_prune_fwd_flashinfer (FlashInfer
+ *     attention with return_lse + _fused_qc_kernel_opt), svoo/co_clustering.py:1801-2050.
+ * ------------------------------------------------------------------------------------------- */
+int svoo_ear_value_stats(const uint16_t* v_perm, const int32_t* k_offsets, const int32_t* k_sizes, int bh, int n,
+                         int kn, int d, int compute_vc, uint16_t* v_cent, float* vc_sq, float* tok_stats,
+                         void* stream);
+int svoo_ear_centroid_logits(const uint16_t* qc, const uint16_t* kc, int bh, int qn, int kn, int d,
+                             uint16_t* c_logits, void* stream);
+int svoo_ear_efficiency(const uint16_t* qc, const uint16_t* k_perm, const uint16_t* c_logits, const float* tok_stats,
+                        const float* vc_sq, const int32_t* q_sizes, const int32_t* k_sizes, const int32_t* k_offsets,
+                        int bh, int n, int qn, int kn, int d, float gamma, float eps, float* eff, void* stream);
+int svoo_ear_select(const uint16_t* c_logits, const float* eff, const int32_t* q_sizes, const int32_t* k_sizes,
+                    const int32_t* preserve, const int32_t* budget_preserve, int b, int h, int qn, int kn,
+                    float p_storage, uint8_t* map, void* stream);
+int svoo_vbsa_ear_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* k_cent,
+                      const uint16_t* v_cent, const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes,
+                      uint16_t* o, int bh, int s, int d, int qn, int kn, void* workspace, size_t ws_bytes,
+                      int32_t* status, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Offline profile producer: exact attention sparsity.
  *   svoo_exact_sparsity_counts: for each of `rows` rows of n bf16 attention scores, the smallest
  *   number of keys whose softmax weights (of scores * scale) hold `threshold` of the row's mass;

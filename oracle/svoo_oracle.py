@@ -52,6 +52,14 @@ __all__ = [
     "sparsity_weights",
     "exact_sparsity_counts",
     "exact_attention_sparsity",
+    "value_centroids",
+    "value_stats",
+    "ear_centroid_logits",
+    "ear_efficiency_scores",
+    "ear_row_params",
+    "ear_select",
+    "ear_compensated_attention",
+    "ear_attention_call",
 ]
 
 _FIX_SHIFT = 60  # fixed-point scale of the top-p prefix sums (2**60)
@@ -740,3 +748,246 @@ def exact_attention_sparsity(query, key, threshold: float = 0.95, query_sample_s
     counts = exact_sparsity_counts(scores, d ** -0.5, threshold)
     per_head = (counts / float(sk)).mean(axis=(0, 2))
     return float(per_head.mean()), per_head.tolist(), counts
+
+
+# --------------------------------------------------------------------------------------
+# EAR: error-aware routing with centroid compensation (svoo/co_clustering.py:1314-2050)
+# --------------------------------------------------------------------------------------
+def value_centroids(v_perm, k_sizes, dtype: str = "bf16") -> np.ndarray:
+    """Mean value row of each key cluster over the cluster-contiguous ``v_perm`` ``[BH, N, D]``
+    (``_compute_value_centroids``, ``svoo/models/wan/attention.py:593-610``): the reference scatter-adds the
+    members into a bf16 tensor and divides by ``bf16(max(count, 1))``.  Contract: the member sum is exact,
+    rounded (via float32) to the storage dtype, then divided in float32 by the storage-rounded count and rounded
+    again; an empty cluster gives 0."""
+    v = np.asarray(v_perm, np.float32)
+    ks = np.asarray(k_sizes, np.int64)
+    bh, _, d = v.shape
+    kn = ks.shape[-1]
+    out = np.zeros((bh, kn, d), np.float32)
+    for b in range(bh):
+        off = np.concatenate([[0], np.cumsum(ks[b])])
+        for j in range(kn):
+            sm = v[b, off[j]:off[j + 1]].astype(np.float64).sum(axis=0)
+            s_st = storage_round(sm.astype(np.float32), dtype).astype(np.float32)
+            den = storage_round(np.float32(max(int(ks[b, j]), 1)), dtype).astype(np.float32)
+            out[b, j] = storage_round((s_st / den).astype(np.float32), dtype)
+    return out
+
+
+def value_stats(v_perm, vc, k_sizes) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Per-token ``|v_t|^2`` and ``vc_j . v_t`` (t in cluster j) and per-cluster ``|vc_j|^2``
+    (``_precompute_v_stats_kernel``, ``co_clustering.py:1315-1396``), in float64."""
+    v = np.asarray(v_perm, np.float64)
+    c = np.asarray(vc, np.float64)
+    ks = np.asarray(k_sizes, np.int64)
+    labels = np.stack([np.repeat(np.arange(ks.shape[-1]), ks[b]) for b in range(ks.shape[0])])
+    vn = (v * v).sum(-1)
+    cvd = np.einsum("bnd,bnd->bn", v, np.take_along_axis(c, labels[..., None], axis=1))
+    return vn, cvd, (c * c).sum(-1)
+
+
+def ear_centroid_logits(qc, kc, dtype: str = "bf16") -> np.ndarray:
+    """``einsum(Qc, Kc) * D**-0.5`` on bf16 tensors (``co_clustering.py:1725``): the bf16 product times the
+    float32 scale, rounded to bf16."""
+    d = np.asarray(qc).shape[-1]
+    s = storage_round(_exact_matmul_nt(qc, kc), dtype)
+    return storage_round((s.astype(np.float32) * np.float32(d ** -0.5)).astype(np.float32), dtype)
+
+
+def ear_efficiency_scores(qc, c_logits, k_perm, v_perm, vc, q_sizes, k_sizes, gamma: float, eps: float = 1e-8):
+    """``log(err_ij) - gamma * log(max(|Q_i| |K_j|, eps))`` (``co_clustering.py:1399-1567``) with
+    ``err_ij = max(sum_t || e^{a_t} v_t - e^{c_ij} vc_j ||^2, eps)`` over the tokens t of key cluster j,
+    ``a_t = (qc_i . k_t) / sqrt(D)`` and ``c_ij`` the bf16 centroid logit; evaluated in float64 with the
+    exponents shifted by ``max(c_ij, max_t a_t)``.  Inputs ``[BH, ...]``; returns float32 ``[BH, Qc, Kc]``."""
+    qc = np.asarray(qc, np.float64)
+    c = np.asarray(c_logits, np.float64)
+    kp = np.asarray(k_perm, np.float64)
+    vp = np.asarray(v_perm, np.float64)
+    vcv = np.asarray(vc, np.float64)
+    qs = np.asarray(q_sizes, np.int64)
+    ks = np.asarray(k_sizes, np.int64)
+    bh, qn, d = qc.shape
+    kn = ks.shape[-1]
+    scale = d ** -0.5
+    out = np.empty((bh, qn, kn), np.float32)
+    for b in range(bh):
+        koff = np.concatenate([[0], np.cumsum(ks[b])])
+        a_all = (qc[b] @ kp[b].T) * scale  # [Qc, N]
+        vn = (vp[b] ** 2).sum(axis=1)
+        for j in range(kn):
+            t0, t1 = koff[j], koff[j + 1]
+            cj = c[b, :, j]
+            if t1 > t0:
+                a = a_all[:, t0:t1]
+                m = np.maximum(cj, a.max(axis=1))
+                e = np.exp(a - m[:, None])
+                cvd = vp[b, t0:t1] @ vcv[b, j]
+                s2 = (e * e * vn[None, t0:t1]).sum(axis=1)
+                x = (e * cvd[None, :]).sum(axis=1)
+            else:
+                m = cj
+                s2 = x = np.zeros(qn)
+            pc = np.exp(cj - m)
+            err = s2 - 2.0 * pc * x + pc * pc * float(vcv[b, j] @ vcv[b, j]) * (t1 - t0)
+            with np.errstate(divide="ignore", invalid="ignore"):
+                lerr = np.where(err > 0, np.log(np.where(err > 0, err, 1.0)) + 2.0 * m, -np.inf)
+            lerr = np.maximum(lerr, np.log(eps))
+            area = np.maximum(qs[b].astype(np.float64) * (t1 - t0), eps)
+            out[b, :, j] = (lerr - gamma * np.log(area)).astype(np.float32)
+    return out
+
+
+def ear_row_params(h: int, kc_num: int, min_kc_ratio=0) -> Tuple[np.ndarray, np.ndarray]:
+    """Per-head ``(preserve, budget_preserve)`` of the EAR selection (``co_clustering.py:1740-1781``):
+    ``max(1, int(r * Kc))`` and ``max(1, int(r * Kc * 2))`` for ``r > 0``, else 0.  A sequence (or tensor)
+    of H ratios is read through float32; one of length 1, or a number, in double precision; any other length
+    gives no minimum."""
+    pre = np.zeros(h, np.int64)
+    bpre = np.zeros(h, np.int64)
+    if isinstance(min_kc_ratio, (int, float, np.floating, np.integer)) or np.ndim(min_kc_ratio) == 0:
+        rs = [float(min_kc_ratio)] * h
+    else:
+        n = len(min_kc_ratio)
+        if n == h:
+            rs = _ratio_list(min_kc_ratio, h)
+        elif n == 1:
+            rs = [float(min_kc_ratio[0])] * h
+        else:
+            rs = [0.0] * h
+    for i, r in enumerate(rs):
+        if r > 0:
+            pre[i] = max(1, int(r * kc_num))
+            bpre[i] = max(1, int(r * kc_num * 2))
+    return pre, bpre
+
+
+def ear_select(eff, c_logits, q_sizes, k_sizes, top_p: float, min_kc_ratio=0, dtype: str = "bf16") -> np.ndarray:
+    """EAR block map (``identify_dynamic_map_estimated``, ``co_clustering.py:1692-1797``), per (b, h, i) row:
+
+    1. budget probabilities ``softmax(bf16(c + bf16(log(bf16(|K_j|) + 1e-8))))`` rounded to bf16, sorted
+       (descending, stable); the budget keeps position 0 and every later position whose predecessor's
+       cumulative probability is ``<= top_p`` (exact fixed-point prefix, rounded to bf16, as the SVOO mask),
+       at least ``budget_preserve`` positions; ``budget = sum |Q_i||K_j|`` over them;
+    2. the first ``preserve`` budget-ordered clusters are guaranteed; ``remaining = max(budget - their area, 0)``;
+    3. the other clusters in descending efficiency order (stable) are kept while the area before them is
+       ``< remaining``.
+    Areas are exact integers (the reference sums them in float32)."""
+    eff = np.asarray(eff, np.float32)
+    c = np.asarray(c_logits, np.float32)
+    qs = np.asarray(q_sizes, np.int64)
+    ks = np.asarray(k_sizes, np.int64)
+    b, h, qn, kn = eff.shape
+    pre, bpre = ear_row_params(h, kn, min_kc_ratio)
+    p_st = storage_round(np.float32(top_p), dtype)
+    # torch.log(kc_sz.to(bf16) + eps): the sum is a bf16 tensor, rounded before the log
+    ks_eps = storage_round(storage_round(ks.astype(np.float32), dtype).astype(np.float32) + np.float32(1e-8), dtype)
+    lks = storage_round(np.log(ks_eps.astype(np.float64)).astype(np.float32), dtype)  # exact log, rounded
+    logits = storage_round(c + lks[:, :, None, :].astype(np.float32), dtype).astype(np.float64)
+    out = np.zeros((b, h, qn, kn), bool)
+    j_idx = np.arange(kn)
+    for bi in range(b):
+        for hi in range(h):
+            for i in range(qn):
+                lg = logits[bi, hi, i]
+                e = np.exp(lg - lg.max())
+                pb = storage_round((e / e.sum()).astype(np.float32), dtype)
+                order = np.lexsort((j_idx, -pb.astype(np.float64)))
+                prefix = np.cumsum(_fixed_point(pb[order]))
+                cum = _prefix_to_bf16(prefix)
+                le = cum[: kn - 1] <= p_st
+                lead = int(np.argmin(le)) if not le.all() else kn - 1
+                length = max(1 + lead, int(bpre[hi]))
+                length = min(length, kn)
+                area = qs[bi, hi, i] * ks[bi, hi]
+                budget = int(area[order[:length]].sum())
+                guar = order[: int(pre[hi])]
+                remaining = max(budget - int(area[guar].sum()), 0)
+                e2 = eff[bi, hi, i].astype(np.float64).copy()
+                e2[guar] = -1e10
+                order2 = np.lexsort((j_idx, -e2))
+                cum2 = np.cumsum(area[order2])
+                keep = (cum2 - area[order2]) < remaining
+                out[bi, hi, i, guar] = True
+                out[bi, hi, i, order2[keep]] = True
+    return out
+
+
+def ear_compensated_attention(q, k, v, k_centroids, v_centroids, dynamic_map, qc_size, kc_size,
+                              compute_dtype=np.float64) -> np.ndarray:
+    """Sparse attention over the active blocks plus centroid compensation of the pruned ones
+    (``dynamic_block_sparse_prune_fwd_flashinfer`` + ``_fused_qc_kernel_opt``, ``co_clustering.py:1801-2050``):
+    query cluster i attends to the tokens of its active key clusters and, for every inactive key cluster j,
+    to the centroid pair ``(Kc_j, Vc_j)`` with logit ``q . Kc_j / sqrt(D) + log(|K_j| + 1e-6)``; one softmax
+    over both.  ``[B, H, S, D]`` in, ``[B, H, S, D]`` out."""
+    q = np.asarray(q)
+    b, h, s, d = q.shape
+    kk_all = np.asarray(k)
+    vv_all = np.asarray(v)
+    kcv = np.asarray(k_centroids)
+    vcv = np.asarray(v_centroids)
+    m = np.asarray(dynamic_map, bool)
+    qs = np.asarray(qc_size).astype(np.int64)
+    ks = np.asarray(kc_size).astype(np.int64)
+    out = np.zeros((b, h, s, d), compute_dtype)
+    scale = float(d) ** -0.5
+    for bi in range(b):
+        for hi in range(h):
+            qoff = np.concatenate([[0], np.cumsum(qs[bi, hi])])
+            koff = np.concatenate([[0], np.cumsum(ks[bi, hi])])
+            kk = kk_all[bi, hi].astype(compute_dtype)
+            vv = vv_all[bi, hi].astype(compute_dtype)
+            kcc = kcv[bi, hi].astype(compute_dtype)
+            vcc = vcv[bi, hi].astype(compute_dtype)
+            bias = np.log(ks[bi, hi].astype(np.float32) + np.float32(1e-6)).astype(compute_dtype)
+            for i in range(qs.shape[-1]):
+                a, e = qoff[i], qoff[i + 1]
+                if e == a:
+                    continue
+                act = np.nonzero(m[bi, hi, i])[0]
+                ina = np.nonzero(~m[bi, hi, i])[0]
+                rows = np.concatenate([np.arange(koff[j], koff[j + 1]) for j in act]) if len(act) else np.zeros(0, np.int64)
+                qi = q[bi, hi, a:e].astype(compute_dtype)
+                keys = np.concatenate([kk[rows], kcc[ina]])
+                vals = np.concatenate([vv[rows], vcc[ina]])
+                sc = (qi @ keys.T) * compute_dtype(scale)
+                sc[:, len(rows):] += bias[ina][None, :]
+                sc -= sc.max(axis=1, keepdims=True)
+                pr = np.exp(sc)
+                pr /= pr.sum(axis=1, keepdims=True)
+                out[bi, hi, a:e] = pr @ vals
+    return out
+
+
+def ear_attention_call(query, key, value, num_q_centroids: int, num_k_centroids: int, kmeans_iters: int,
+                       top_p: float, min_kc_ratio=0, gamma: float = 1.0, *, init_q_idx=None, init_k_idx=None,
+                       init_q_centroids=None, init_k_centroids=None, dtype: str = "bf16", attn_dtype=np.float64,
+                       return_parts: bool = False):
+    """One EAR ``attention_core_logic`` call (``svoo/models/wan/attention.py:1040-1071, 1180-1215``):
+    co-cluster, permute, value centroids by key label, EAR block map, compensated sparse attention, inverse
+    permutation, ``[1, S, H*D]``."""
+    q = np.asarray(query, np.float32)
+    k = np.asarray(key, np.float32)
+    v = np.asarray(value, np.float32)
+    b, h, s, d = q.shape
+    assert b == 1
+    ql, qcent, qsz, kl, kcent, ksz = co_cluster_tokens(q[0], k[0], num_q_centroids, num_k_centroids, kmeans_iters,
+                                                       init_q_idx=init_q_idx, init_k_idx=init_k_idx,
+                                                       init_q_centroids=init_q_centroids,
+                                                       init_k_centroids=init_k_centroids, dtype=dtype)
+    qidx, _, _ = cluster_sort(ql, num_q_centroids)
+    kidx, _, _ = cluster_sort(kl, num_k_centroids)
+    qp = permute_rows(q[0], qidx)
+    kp = permute_rows(k[0], kidx)
+    vp = permute_rows(v[0], kidx)
+    vc = value_centroids(vp, ksz, dtype)
+    c = ear_centroid_logits(qcent, kcent, dtype)
+    eff = ear_efficiency_scores(qcent, c, kp, vp, vc, qsz, ksz, gamma)
+    dmap = ear_select(eff[None], c[None], qsz[None], ksz[None], top_p, min_kc_ratio, dtype)
+    op = ear_compensated_attention(qp[None], kp[None], vp[None], kcent[None], vc[None], dmap, qsz[None], ksz[None],
+                                   attn_dtype)[0]
+    o = unpermute_rows(op, qidx)
+    out = o.transpose(1, 0, 2).reshape(1, s, h * d)
+    if return_parts:
+        return out, dict(map=dmap, eff=eff, c=c, vc=vc, qsizes=qsz, ksizes=ksz, qidx=qidx, kidx=kidx,
+                         qcent=qcent, kcent=kcent, qlabels=ql, klabels=kl)
+    return out

@@ -18,6 +18,9 @@
 //     units are busy at the same time;
 //   * fp32 online softmax (exp2 with the scale folded in), P rounded to bf16 for the PV MFMA, as
 //     the reference's Triton kernel does; rows of a cluster with no active keys are written as 0.
+// EAR variant (centroid compensation): the KV stream continues after the active tokens with the
+// (key, value) centroids of the inactive clusters, each scored q . kc_j / sqrt(D) + log(|K_j| + 1e-6),
+// so one online softmax covers both (the reference's token attention + log-sum-exp merge).
 #include "svoo_common.h"
 
 namespace svoo {
@@ -135,6 +138,28 @@ __device__ __forceinline__ int build_segments(const uint8_t* __restrict__ mrow, 
   return nseg;
 }
 
+// EAR: compacts the inactive key clusters of one map row (ascending) with their score bias
+// log2(e) * log(|K_j| + 1e-6) into LDS.  Returns their count.
+__device__ __forceinline__ int build_centroids(const uint8_t* __restrict__ mrow, const int32_t* __restrict__ ksb,
+                                               int kn, int32_t* cent_idx, float* cent_bias, long long* red) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int per = (kn + nt - 1) / nt;
+  const int j0 = min(kn, tid * per), j1 = min(kn, j0 + per);
+  long long loc = 0;
+  for (int j = j0; j < j1; ++j) loc += mrow[j] ? 0 : 1;
+  long long tot;
+  int idx = (int)block_exclusive_scan_i64<kVWaves * kWave>(loc, red, &tot);
+  for (int j = j0; j < j1; ++j) {
+    if (!mrow[j]) {
+      cent_idx[idx] = j;
+      cent_bias[idx] = 1.4426950408889634f * logf((float)ksb[j] + 1e-6f);
+      ++idx;
+    }
+  }
+  __syncthreads();
+  return (int)tot;
+}
+
 // Segment containing stream position p (seg_cum ascending, seg_cum[0] == 0).
 __device__ __forceinline__ int find_segment(const int32_t* seg_cum, int nseg, int p) {
   int lo = 0, hi = nseg - 1;
@@ -192,9 +217,10 @@ __device__ __forceinline__ int cursor_row(KvCursor& c, const int32_t* seg_start,
 // K(t+1) Q^T} and a VALU phase V(t) = {softmax of S(t) -> P(t)}; group B runs one half-step behind
 // group A, so in every half-step one wave per SIMD does MFMA work while the other does VALU work.
 // Group B also issues the LDS DMA of the next K/V tiles and resolves their token rows.
-template <int QB>
+template <int QB, bool EAR>
 __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) vbsa_attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint8_t* __restrict__ map, const int32_t* __restrict__ ks, uint16_t* __restrict__ o, int s, int qn, int kn,
     int cap, long long total_items, const int32_t* __restrict__ qoff, const int32_t* __restrict__ koff,
     const int32_t* __restrict__ items, const int32_t* __restrict__ nitems, float scale_log2) {
@@ -205,7 +231,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   __shared__ __attribute__((aligned(16))) uint16_t v_s0[kKT * 128], v_s1[kKT * 128];
   __shared__ long long red[kVWaves];
   __shared__ int32_t rowtab[2][2][kKT];  // [K/V][slot][tile position] -> token row
-  extern __shared__ int32_t seg_mem[];  // seg_start[kn], seg_cum[kn + 1]
+  extern __shared__ int32_t seg_mem[];  // seg_start[kn], seg_cum[kn + 1] (EAR: cent_idx[kn], cent_bias[kn])
 
   const long long item = xcd_item(blockIdx.x);
   if (item >= total_items) return;
@@ -226,15 +252,25 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   const uint16_t* kb = k + head;
   const uint16_t* vb = v + head;
   uint16_t* ob = o + head;
+  const uint16_t* kcb = EAR ? kc + (size_t)b * kn * 128 : nullptr;
+  const uint16_t* vcb = EAR ? vc + (size_t)b * kn * 128 : nullptr;
 
   int32_t* seg_start = seg_mem;
   int32_t* seg_cum = seg_mem + kn;
+  int32_t* cent_idx = seg_cum + kn + 1;
+  float* cent_bias = (float*)(cent_idx + kn);
   int total = 0;
-  const int nseg_v = build_segments(map + ((size_t)b * qn + ci) * kn, koff + (size_t)b * (kn + 1), ks + (size_t)b * kn,
-                                  kn, seg_start, seg_cum, red, &total);
+  const uint8_t* mrow = map + ((size_t)b * qn + ci) * kn;
+  const int nseg_v = build_segments(mrow, koff + (size_t)b * (kn + 1), ks + (size_t)b * kn, kn, seg_start, seg_cum,
+                                    red, &total);
   // Segment count and stream length are block-uniform: keep them scalar so tile-loop branches are uniform.
   const int nseg = __builtin_amdgcn_readfirstlane(nseg_v);
   total = __builtin_amdgcn_readfirstlane(total);
+  const int total_tok = total;  // keys of the active clusters; EAR appends the inactive centroids
+  if constexpr (EAR) {
+    const int ncent = build_centroids(mrow, ks + (size_t)b * kn, kn, cent_idx, cent_bias, red);
+    total = __builtin_amdgcn_readfirstlane(total_tok + ncent);
+  }
 
   if (total == 0) {
     // Empty row: zero output (reference semantics, svoo/co_clustering.py:1102-1104).
@@ -260,20 +296,29 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   float m_run = -INFINITY, l_run = 0.0f;
 
   // Row tables: wave 4 resolves K tiles, wave 5 V tiles (lane = tile position).
-  const int last_row = seg_start[nseg - 1] + (total - 1 - seg_cum[nseg - 1]);
+  // Rows past the stream repeat its last token row (0 when an EAR row has no active tokens); EAR
+  // centroid j is entered as row -1 - j.
+  const int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
   KvCursor cursor;
-  if (wave == 4 || wave == 5) cursor_init(cursor, seg_start, seg_cum, nseg, min(lane, total - 1));
+  if ((wave == 4 || wave == 5) && nseg > 0) cursor_init(cursor, seg_start, seg_cum, nseg, min(lane, total_tok - 1));
   auto resolve = [&](int32_t* tab, int t) {
     const int p = t * kKT + lane;
-    tab[lane] = p < total ? cursor_row(cursor, seg_start, seg_cum, p) : last_row;
+    if (p < total_tok)
+      tab[lane] = cursor_row(cursor, seg_start, seg_cum, p);
+    else if (EAR && p < total)
+      tab[lane] = -1 - cent_idx[p - total_tok];
+    else
+      tab[lane] = last_row;
   };
   // DMA mapping (group B): wave 4+w, group j moves tile rows 4(kDmaIt w + j) + lane/16.
   const int prow = lane / 16, pch = lane % 16;
-  auto dma = [&](const uint16_t* src, const int32_t* tab, uint16_t* buf) {
+  auto dma = [&](const uint16_t* src, const uint16_t* csrc, const int32_t* tab, uint16_t* buf) {
 #pragma unroll
     for (int j = 0; j < kDmaIt; ++j) {
       const int r = 4 * (kDmaIt * wg + j) + prow;
-      lds_dma16(src + (size_t)tab[r] * 128 + swz(r, pch) * 8, buf + 4 * (kDmaIt * wg + j) * 128);
+      const int tr = tab[r];
+      const uint16_t* rp = (EAR && tr < 0) ? csrc + (size_t)(-1 - tr) * 128 : src + (size_t)tr * 128;
+      lds_dma16(rp + swz(r, pch) * 8, buf + 4 * (kDmaIt * wg + j) * 128);
     }
   };
 
@@ -325,22 +370,43 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   };
   // VALU phase V(t): online softmax of S(t) -> bf16 P(t) (per lane: one query, 32 of 64 keys).
   auto vphase = [&](int t) {
-    if ((t + 1) * kKT > total) {
-      const int tbase = t * kKT;
+    // sl: the factor from sacc to log2-domain logits (1 once an EAR tile is pre-scaled and biased)
+    float sl = scale_log2;
+    if constexpr (EAR) {
+      if ((t + 1) * kKT > total_tok) {
+        const int tbase = t * kKT;
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2)
+        for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
-          if (tbase + key >= total) sacc[kb2][r] = -INFINITY;
-        }
+          for (int r = 0; r < 16; ++r) {
+            const int p = tbase + kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+            float xv = sacc[kb2][r] * scale_log2;
+            if (p >= total)
+              xv = -INFINITY;
+            else if (p >= total_tok)
+              xv += cent_bias[p - total_tok];
+            sacc[kb2][r] = xv;
+          }
+        sl = 1.0f;
+      }
+    } else {
+      if ((t + 1) * kKT > total) {
+        const int tbase = t * kKT;
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kb2 * 32 + (r / 4) * 8 + h * 4 + (r % 4);
+            if (tbase + key >= total) sacc[kb2][r] = -INFINITY;
+          }
+      }
     }
     float mx = sacc[0][0];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb2][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * sl;
     if (__any(mx > m_run + 8.0f)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -358,7 +424,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       float pv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][r], scale_log2, mneg));
+        pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][r], sl, mneg));
         ls += pv[r];
       }
 #pragma unroll
@@ -370,8 +436,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   };
   // Group B housekeeping at the start of its V(t): DMA K(t+2), V(t+1); resolve K(t+3), V(t+2).
   auto fetch = [&](int t, uint16_t* kdst, uint16_t* vdst) {
-    if (t + 2 < ntiles) dma(kb, rowtab[0][t & 1], kdst);
-    if (t + 1 < ntiles) dma(vb, rowtab[1][(t + 1) & 1], vdst);
+    if (t + 2 < ntiles) dma(kb, kcb, rowtab[0][t & 1], kdst);
+    if (t + 1 < ntiles) dma(vb, vcb, rowtab[1][(t + 1) & 1], vdst);
     if (wave == 4 && t + 3 < ntiles) resolve(rowtab[0][(t + 1) & 1], t + 3);
     if (wave == 5 && t + 2 < ntiles) resolve(rowtab[1][t & 1], t + 2);
   };
@@ -388,9 +454,9 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   }
   __syncthreads();
   if (group_b) {
-    dma(kb, rowtab[0][0], k_s0);
-    dma(vb, rowtab[1][0], v_s0);
-    if (ntiles > 1) dma(kb, rowtab[0][1], k_s1);
+    dma(kb, kcb, rowtab[0][0], k_s0);
+    dma(vb, vcb, rowtab[1][0], v_s0);
+    if (ntiles > 1) dma(kb, kcb, rowtab[0][1], k_s1);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   __syncthreads();
@@ -516,17 +582,21 @@ extern "C" size_t svoo_vbsa_workspace_size(int bh, int s, int qn, int kn) {
   return vbsa_layout(bh, s, qn, kn).total;
 }
 
-extern "C" int svoo_vbsa_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint8_t* map,
-                             const int32_t* q_sizes, const int32_t* k_sizes, uint16_t* o, int bh, int s, int d, int qn,
-                             int kn, void* workspace, size_t ws_bytes, int32_t* status, void* stream) {
-  SVOO_REQUIRE(q && k && v && map && q_sizes && k_sizes && o, SVOO_ERR_INVALID_ARG, "svoo_vbsa_fwd: null pointer");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_vbsa_fwd: D=%d (only 128 supported)", d);
-  SVOO_REQUIRE(bh > 0 && s > 0 && qn > 0 && kn > 0, SVOO_ERR_INVALID_ARG, "svoo_vbsa_fwd: bad dims");
-  SVOO_REQUIRE(kn <= kMaxKN && qn < 32768, SVOO_ERR_UNSUPPORTED, "svoo_vbsa_fwd: qn=%d kn=%d above limits", qn, kn);
-  SVOO_REQUIRE((long long)bh * s * 128 < (1ll << 40), SVOO_ERR_UNSUPPORTED, "svoo_vbsa_fwd: too large");
+namespace {
+template <bool EAR>
+int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* kc,
+                const uint16_t* vc, const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes, uint16_t* o,
+                int bh, int s, int d, int qn, int kn, void* workspace, size_t ws_bytes, int32_t* status,
+                void* stream) {
+  SVOO_REQUIRE(q && k && v && map && q_sizes && k_sizes && o && (!EAR || (kc && vc)), SVOO_ERR_INVALID_ARG,
+               "%s: null pointer", name);
+  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "%s: D=%d (only 128 supported)", name, d);
+  SVOO_REQUIRE(bh > 0 && s > 0 && qn > 0 && kn > 0, SVOO_ERR_INVALID_ARG, "%s: bad dims", name);
+  SVOO_REQUIRE(kn <= kMaxKN && qn < 32768, SVOO_ERR_UNSUPPORTED, "%s: qn=%d kn=%d above limits", name, qn, kn);
+  SVOO_REQUIRE((long long)bh * s * 128 < (1ll << 40), SVOO_ERR_UNSUPPORTED, "%s: too large", name);
   const VbsaWs lay = vbsa_layout(bh, s, qn, kn);
-  SVOO_REQUIRE(lay.cap < 65536, SVOO_ERR_UNSUPPORTED, "svoo_vbsa_fwd: too many q tiles per head");
-  SVOO_REQUIRE(workspace && ws_bytes >= lay.total, SVOO_ERR_WORKSPACE, "svoo_vbsa_fwd: workspace %zu < %zu", ws_bytes,
+  SVOO_REQUIRE(lay.cap < 65536, SVOO_ERR_UNSUPPORTED, "%s: too many q tiles per head", name);
+  SVOO_REQUIRE(workspace && ws_bytes >= lay.total, SVOO_ERR_WORKSPACE, "%s: workspace %zu < %zu", name, ws_bytes,
                lay.total);
   hipStream_t st = (hipStream_t)stream;
   char* base = (char*)workspace;
@@ -537,15 +607,32 @@ extern "C" int svoo_vbsa_fwd(const uint16_t* q, const uint16_t* k, const uint16_
   constexpr int qtile = VbsaCfg<kDefaultQB>::kQTile;
   hipLaunchKernelGGL(vbsa_plan_kernel, dim3(bh), dim3(kPlanThreads), 0, st, q_sizes, k_sizes, s, qn, kn, qtile, lay.cap,
                      qoff, koff, items, nitems, status);
-  if (int rc = check_launch("svoo_vbsa_fwd(plan)")) return rc;
+  if (int rc = check_launch(name)) return rc;
   const long long total_items = (long long)bh * lay.cap;
   const long long nblocks = (total_items + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
-  SVOO_REQUIRE(nblocks < (1ll << 31), SVOO_ERR_UNSUPPORTED, "svoo_vbsa_fwd: too many work items");
+  SVOO_REQUIRE(nblocks < (1ll << 31), SVOO_ERR_UNSUPPORTED, "%s: too many work items", name);
   const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)d));
-  const size_t smem = (size_t)(2 * kn + 1) * sizeof(int32_t);
-  hipLaunchKernelGGL(vbsa_attn_kernel<kDefaultQB>, dim3((unsigned)nblocks), dim3(kVWaves * kWave), smem, st, q, k, v,
-                     map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items, nitems, scale_log2);
-  return check_launch("svoo_vbsa_fwd");
+  const size_t smem = (size_t)((EAR ? 4 : 2) * kn + 1) * sizeof(int32_t);
+  hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR>), dim3((unsigned)nblocks), dim3(kVWaves * kWave), smem, st, q,
+                     k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items, nitems,
+                     scale_log2);
+  return check_launch(name);
+}
+}  // namespace
+
+extern "C" int svoo_vbsa_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint8_t* map,
+                             const int32_t* q_sizes, const int32_t* k_sizes, uint16_t* o, int bh, int s, int d, int qn,
+                             int kn, void* workspace, size_t ws_bytes, int32_t* status, void* stream) {
+  return vbsa_launch<false>("svoo_vbsa_fwd", q, k, v, nullptr, nullptr, map, q_sizes, k_sizes, o, bh, s, d, qn, kn,
+                            workspace, ws_bytes, status, stream);
+}
+
+extern "C" int svoo_vbsa_ear_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* k_cent,
+                                 const uint16_t* v_cent, const uint8_t* map, const int32_t* q_sizes,
+                                 const int32_t* k_sizes, uint16_t* o, int bh, int s, int d, int qn, int kn,
+                                 void* workspace, size_t ws_bytes, int32_t* status, void* stream) {
+  return vbsa_launch<true>("svoo_vbsa_ear_fwd", q, k, v, k_cent, v_cent, map, q_sizes, k_sizes, o, bh, s, d, qn, kn,
+                           workspace, ws_bytes, status, stream);
 }
 
 extern "C" int svoo_vbsa_segments(const uint8_t* map, const int32_t* k_sizes, int bh, int qn, int kn,

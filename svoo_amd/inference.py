@@ -1,9 +1,9 @@
 """Install the SVOO attention processors into a Wan pipeline (the reference's configuration surface).
 
-``replace_wan_attention`` follows ``svoo/models/wan/inference.py:23-369`` (SAP branch): it derives the
-token geometry from the pipeline, writes the SVOO configuration as class attributes of
-:class:`WanAttn_SAPAttn_Processor` (shared by every layer, as in the reference) and registers one
-processor instance per transformer block (``transformer_2`` too, for Wan2.2).  The pipeline is
+``replace_wan_attention`` follows ``svoo/models/wan/inference.py:23-440`` (the SAP, EAR and dense
+patterns): it derives the token geometry from the pipeline, writes the configuration as class
+attributes of the pattern's processor class (shared by every layer, as in the reference) and
+registers one processor instance per transformer block (``transformer_2`` too, for Wan2.2).  The pipeline is
 duck-typed: ``pipe.transformer.blocks[i].attn1.set_processor``, ``pipe.transformer.config``
 (``patch_size``, ``num_attention_heads``, ``attention_head_dim``) and ``pipe.vae_scale_factor_*``.
 No kernel warm-up is needed: the HIP kernels are compiled ahead of time.
@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import os
 
-from .processor import WanAttn_SAPAttn_Processor
+from .processor import WanAttn_DenseAttn_Processor, WanAttn_EARAttn_Processor, WanAttn_SAPAttn_Processor
 from .sparsity import SparsityLookup
 
 
@@ -41,6 +41,7 @@ def replace_wan_attention(
     top_p_kmeans=None,
     min_kc_ratio=0,
     max_kc_ratio=0,
+    ear_gamma=1.0,
     kmeans_iter_init=0,
     kmeans_iter_step=0,
     zero_step_kmeans_init=False,
@@ -59,29 +60,37 @@ def replace_wan_attention(
     sparsity_query_samples=0,
     sparsity_threshold=0.95,
     sparsity_start_step=1,
-    processor_cls=WanAttn_SAPAttn_Processor,
+    processor_cls=None,
     **unused,
 ):
     """Configure SVOO attention and install one processor per Wan DiT block.
 
     Arguments keep the reference's names and meaning (``svoo/models/wan/inference.py:23-74``);
     ``first_layers_fp`` is a layer count and ``first_times_fp`` a timestep threshold, as the CLI
-    passes them.  ``max_kc_ratio`` is forwarded to the mask.  Only the SVOO ``"SAP"`` pattern is
-    built here: other patterns raise ``ValueError`` as the reference does for unsupported ones, and
-    the EAR / global-constraint / routing variants raise ``NotImplementedError``.  A missing or
-    unreadable profile CSV disables the dynamic ratios (``:308-320``).  With
-    ``measure_attention_sparsity`` every processor also appends the exact per-head sparsity of each
-    (layer, step) to ``sparsity_output_file`` (the offline profile producer).  Returns the processors.
+    passes them.  ``max_kc_ratio`` is forwarded to the SAP mask (EAR has no cap).  Patterns:
+    ``"SAP"`` (:class:`WanAttn_SAPAttn_Processor`), ``"EAR"`` (:class:`WanAttn_EARAttn_Processor`, with
+    ``ear_gamma``) and the ``"dense"`` diagnostic (:class:`WanAttn_DenseAttn_Processor`: dense attention,
+    used to record sparsity profiles); anything else, or ``use_svoo=False``, raises ``ValueError`` as the
+    reference does (``:77-78``), and the global-constraint / routing variants raise
+    ``NotImplementedError``.  ``processor_cls`` overrides the pattern's class (a subclass keeps the
+    configuration local to it).  A missing or unreadable profile CSV disables the dynamic ratios
+    (``:308-320``).  With ``measure_attention_sparsity`` every processor also appends the exact per-head
+    sparsity of each (layer, step) to ``sparsity_output_file`` (the offline profile producer).  Returns the
+    processors.
     """
-    if pattern != "SAP" or not use_svoo:
-        raise ValueError("Only the SVOO SAP pattern is supported by this build (pattern='SAP', use_svoo=True).")
+    if pattern not in ("SAP", "EAR", "dense") or not use_svoo:
+        raise ValueError("Only SVOO, EAR and dense diagnostic patterns are supported in this release.")
     if use_global_constraints or use_routing_transformer_strategy:
         raise NotImplementedError("global-constraint and routing-transformer variants are not built here")
     num_frame_patches, frame_patches_one_frame = wan_token_geometry(pipe, height, width, num_frames)
     blocks = pipe.transformer.blocks
     num_layers = len(blocks)
 
-    cls = processor_cls
+    cls = processor_cls or {"SAP": WanAttn_SAPAttn_Processor, "EAR": WanAttn_EARAttn_Processor,
+                            "dense": WanAttn_DenseAttn_Processor}[pattern]
+    if pattern != "dense":
+        cls.use_ear = pattern == "EAR"  # inference.py:282
+        cls.ear_gamma = ear_gamma
     cls.first_layers_fp = first_layers_fp
     cls.first_times_fp = first_times_fp
     cls.context_length = 0

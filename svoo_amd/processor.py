@@ -11,6 +11,10 @@ configuration of ``svoo/models/wan/attention.py:546-1216``:
   co-clustering (or the reuse cache), per-head profile ratios, block mask, permutes, variable-block
   sparse attention and the inverse permutation.
 
+``WanAttn_EARAttn_Processor`` swaps the top-p mask for EAR routing (an area budget filled by estimated
+pruning error) and the attention for its centroid-compensated form
+(``svoo/models/wan/attention.py:1047-1071, 1180-1196, 1219-1222``).
+
 ``Hunyuan_SAPAttn_Processor`` adds the text-dense post-processing of
 ``svoo/models/hunyuan10/attention.py:977-1110`` on the same kernels.
 """
@@ -24,6 +28,7 @@ import torch
 import torch.nn.functional as F
 
 from .co_clustering import block_mask_lengths, co_cluster_tokens_full, dynamic_block_sparse_fwd
+from .ear import dynamic_block_sparse_prune_fwd, ear_map_and_value_centroids
 from .sparsity.exact import compute_exact_attention_sparsity, format_sparsity_log, has_completed_sparsity_entry
 from .permute import apply_inverse_permutation, apply_inverse_permutation_bshd, permute_pair_by_indices
 from . import _lib
@@ -85,9 +90,11 @@ class WanAttn_SAPAttn_Processor:
     sparsity_lookup = None
     dynamic_min_kc_ratio_min = None
     dynamic_min_kc_ratio_max = None
-    # Variants of the reference that this build does not carry (see DESIGN.md scope).
+    # Variants: EAR routing is built (WanAttn_EARAttn_Processor); the global-constraint and
+    # routing-transformer clusterings are not.
     use_svoo = True
     use_ear = False
+    ear_gamma = 1.0
     use_global_constraints = False
     use_routing_transformer_strategy = False
     enable_mem_save = bool(int(os.environ.get("SVOO_ENABLE_MEM_SAVE", "1")))
@@ -251,8 +258,8 @@ class WanAttn_SAPAttn_Processor:
     def _check_variant(self):
         if not self.use_svoo:
             raise ValueError("Only the SVOO co-clustering path is supported (use_svoo=True).")
-        if self.use_ear or self.use_global_constraints or self.use_routing_transformer_strategy:
-            raise NotImplementedError("EAR, global-constraint and routing-transformer variants are not built here.")
+        if self.use_global_constraints or self.use_routing_transformer_strategy:
+            raise NotImplementedError("global-constraint and routing-transformer variants are not built here.")
 
     def _co_cluster(self, query, key, iters, warm):
         cfg, num_heads, seq_len, dim = query.size()
@@ -318,7 +325,8 @@ class WanAttn_SAPAttn_Processor:
     def semantic_aware_permutation(self, query, key, value, timestep=None):
         """Cluster, build the block map and permute Q/K/V (``svoo/models/wan/attention.py:958-1088``).
 
-        Returns ``(q_perm, k_perm, v_perm, dynamic_map, q_cluster_sizes, k_cluster_sizes, q_sorted_indices)``.
+        Returns ``(q_perm, k_perm, v_perm, dynamic_map, q_cluster_sizes, k_cluster_sizes, q_sorted_indices)``,
+        with EAR also ``(k_centroids, v_centroids)``.
         """
         cfg, num_heads, seq_len, dim = query.size()
         r = self.kmeans_clustering(query, key, self.layer_idx)
@@ -329,6 +337,16 @@ class WanAttn_SAPAttn_Processor:
         q_perm = _permute_rows(query, r["q_sorted_idx"])
         k_perm, v_perm = permute_pair_by_indices(key, value, r["k_sorted_idx"])
         self._mark("permute")
+        if self.use_ear:
+            qcv = r["qcentroids"].view(cfg, num_heads, self.num_q_centroids, dim)
+            kcv = r["kcentroids"].view(cfg, num_heads, self.num_k_centroids, dim)
+            v_cent, dynamic_map, parts = ear_map_and_value_centroids(
+                q_perm, k_perm, v_perm, q_sizes, k_sizes, qcv, kcv, self.top_p_kmeans, gamma=self.ear_gamma,
+                min_kc_ratio=min_kc_ratio, return_parts=True)
+            self._last_call = dict(clustering=r, map=dynamic_map, lengths=dynamic_map.sum(-1, dtype=torch.int32),
+                                   min_kc_ratio=min_kc_ratio, q_sizes=q_sizes, k_sizes=k_sizes, v_centroids=v_cent,
+                                   **parts)
+            return q_perm, k_perm, v_perm, dynamic_map, q_sizes, k_sizes, r["q_sorted_idx"], kcv, v_cent
         dynamic_map, lengths = block_mask_lengths(
             r["qcentroids"].view(cfg, num_heads, self.num_q_centroids, dim),
             r["kcentroids"].view(cfg, num_heads, self.num_k_centroids, dim),
@@ -369,16 +387,41 @@ class WanAttn_SAPAttn_Processor:
             return out.transpose(1, 2).flatten(2, 3)
 
         self._mark("start")
-        q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, q_sorted_indices = self.semantic_aware_permutation(
-            query, key, value, timestep)
+        perm = self.semantic_aware_permutation(query, key, value, timestep)
+        q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, q_sorted_indices = perm[:7]
         self._mark("mask")
-        out_perm = dynamic_block_sparse_fwd(q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, validate=False)
+        if len(perm) == 9:  # EAR: centroid-compensated attention
+            out_perm = dynamic_block_sparse_prune_fwd(q_perm, k_perm, v_perm, perm[7], perm[8], dyn_map, qc_sz, kc_sz,
+                                                      validate=False)
+        else:
+            out_perm = dynamic_block_sparse_fwd(q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, validate=False)
         self._mark("attention")
         if self.enable_mem_save:
             del q_perm, k_perm, v_perm
         out = apply_inverse_permutation_bshd(out_perm, q_sorted_indices)
         self._mark("unpermute")
         return out
+
+
+class WanAttn_EARAttn_Processor(WanAttn_SAPAttn_Processor):
+    """Wan SAP processor with EAR (error-aware routing, centroid compensation) enabled
+    (``svoo/models/wan/attention.py:1219-1222``)."""
+
+    use_ear = True
+
+
+class WanAttn_DenseAttn_Processor(WanAttn_SAPAttn_Processor):
+    """Dense self-attention on every layer and step, with the optional sparsity logging: the
+    ``pattern="dense"`` diagnostic that produces the per-head profiles (``svoo/models/wan/inference.py:398-440``
+    with ``WanAttn_SVGAttn_Processor2_0.attention_core_logic`` and ``attention_masks = None``,
+    ``svoo/models/wan/attention.py:337-355``)."""
+
+    def attention_core_logic(self, query, key, value, timestep):
+        cfg, num_heads, seq_len, dim = query.size()
+        assert seq_len == self.context_length + self.num_frame * self.frame_size, (
+            f"Query Shape: {seq_len} is not equivalent to {self.context_length} + {self.num_frame} * {self.frame_size}"
+        )
+        return self.flash_attention(query, key, value).transpose(1, 2).flatten(2, 3)
 
 
 def _apply_rotary_emb_real(x: torch.Tensor, freqs_cis) -> torch.Tensor:

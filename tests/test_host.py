@@ -224,6 +224,38 @@ def test_replace_wan_attention_fallbacks_and_rejections():
         replace_wan_attention(pipe, 480, 832, 81, 0, 900, use_global_constraints=True, processor_cls=cls)
 
 
+def test_replace_wan_attention_ear_and_dense_patterns():
+    from svoo_amd.inference import replace_wan_attention
+    from svoo_amd.processor import WanAttn_DenseAttn_Processor, WanAttn_EARAttn_Processor, WanAttn_SAPAttn_Processor
+
+    pipe = _tiny_pipe()
+    cls = type("E", (WanAttn_EARAttn_Processor,), {})
+    procs = replace_wan_attention(pipe, 480, 832, 81, 0, 900, pattern="EAR", num_q_centroids=8, num_k_centroids=16,
+                                  top_p_kmeans=0.9, min_kc_ratio=0.1, ear_gamma=0.5, processor_cls=cls)
+    assert all(isinstance(p, cls) for p in procs)
+    assert cls.use_ear and cls.ear_gamma == 0.5 and cls.num_frame == 21
+    assert not WanAttn_SAPAttn_Processor.use_ear and WanAttn_EARAttn_Processor.use_ear
+    sap = type("S", (WanAttn_EARAttn_Processor,), {})
+    replace_wan_attention(pipe, 480, 832, 81, 0, 900, pattern="SAP", num_q_centroids=8, num_k_centroids=16,
+                          top_p_kmeans=0.9, processor_cls=sap)
+    assert not sap.use_ear  # inference.py:282 sets use_ear from the pattern
+    # "dense": the diagnostic processor class (dense attention on every layer)
+    procs = replace_wan_attention(pipe, 480, 832, 81, 0, 900, pattern="dense")
+    assert all(type(p) is WanAttn_DenseAttn_Processor for p in procs)
+
+
+@pytest.mark.parametrize("ratio", [0, 0.0, 0.1, 0.35, [0.1], [0.0, 0.05, 0.35], [0.2, 0.3], (0.25, 0.5, 0.01)])
+def test_ear_row_params_matches_oracle(ratio):
+    from svoo_amd.ear import ear_row_params
+
+    for kn in (16, 100, 1000):
+        pre, bpre = ear_row_params(3, kn, ratio)
+        opre, obpre = O.ear_row_params(3, kn, ratio)
+        assert pre == list(opre) and bpre == list(obpre), (ratio, kn)
+    pre, bpre = ear_row_params(3, 100, torch.tensor([0.0, 0.05, 0.35]))
+    assert (pre, bpre) == ([0, 5, 34], [0, 10, 69])  # float32 reads of a tensor (0.35 -> 0.34999999)
+
+
 def test_tiny_dit_dense_forward_shapes():
     from svoo_amd import dit
 
