@@ -47,6 +47,9 @@ def parse_args():
                     help="C2-C4: one SVOO attention call; C5: one denoising step of a random-init Wan2.1-1.3B DiT")
     ap.add_argument("--mode", default="density", choices=["density", "reference"],
                     help="density: top_p=0, min_kc_ratio=rho_h; reference: top_p=0.9, min_kc_ratio=clip(rho_h,0.15,0.2)")
+    ap.add_argument("--pattern", default="SAP", choices=["SAP", "EAR"],
+                    help="SAP: top-p block mask (the headline); EAR: error-aware routing with centroid compensation "
+                         "(Wan configs)")
     ap.add_argument("--sparsity-profile", action="store_true",
                     help="time the offline profile producer (exact per-head sparsity of one layer) instead")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
@@ -87,7 +90,7 @@ def main():
 
     from svoo_amd import _lib, synth
     from svoo_amd.co_clustering import co_cluster_tokens_full
-    from svoo_amd.processor import Hunyuan_SAPAttn_Processor, WanAttn_SAPAttn_Processor
+    from svoo_amd.processor import Hunyuan_SAPAttn_Processor, WanAttn_EARAttn_Processor, WanAttn_SAPAttn_Processor
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a HIP device")
@@ -98,8 +101,12 @@ def main():
     qcn, kcn, iters = cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters
     hunyuan = cfg.text_tokens > 0
     nv = cfg.video_tokens
+    ear = args.pattern == "EAR"
+    if ear and hunyuan:
+        raise SystemExit("EAR is wired for the Wan processor only (as in the reference)")
 
-    log(f"config {cfg.name}: H={h} N={n} d={d} Qc={qcn} Kc={kcn} iters={iters} mode={args.mode}")
+    log(f"config {cfg.name}: H={h} N={n} d={d} Qc={qcn} Kc={kcn} iters={iters} mode={args.mode} "
+        f"pattern={args.pattern}")
     t0 = time.time()
     q, k, v = synth.make_qkv_device(cfg, dev)
     torch.cuda.synchronize()
@@ -122,7 +129,8 @@ def main():
     k_init = synth.perturb_centroids(cfg, prev["kcentroids"], 4)
     del prev
 
-    class Proc(Hunyuan_SAPAttn_Processor if hunyuan else WanAttn_SAPAttn_Processor):
+    class Proc(Hunyuan_SAPAttn_Processor if hunyuan else (WanAttn_EARAttn_Processor if ear else
+                                                         WanAttn_SAPAttn_Processor)):
         pass
 
     Proc.num_frame, Proc.frame_size = cfg.frames, cfg.frame_size
@@ -183,7 +191,9 @@ def main():
     ks = last["k_sizes"].to(torch.int64)
     dmap = last["map"]
     pairs = int((dmap.to(torch.int64) * qs[..., :, None] * ks[..., None, :]).sum().item())
-    active_flop = 4.0 * d * pairs
+    # EAR: every query row also scores the centroids of its inactive clusters
+    cent_pairs = int(((~dmap).to(torch.int64).sum(-1) * qs).sum().item()) if ear else 0
+    active_flop = 4.0 * d * (pairs + cent_pairs)
     dense_flop = cfg.dense_flops()
     realized_density = pairs / (h * float(n) ** 2)
     active_tflops = active_flop / (attn_ms_avg * 1e-3) / 1e12
@@ -244,7 +254,7 @@ def main():
             log(f"traffic file unreadable: {e!r}")
 
     roofline = {
-        "kernel": "vbsa_attn_kernel",
+        "kernel": "vbsa_attn_kernel" + ("<EAR>" if ear else ""),
         "bound": "mfma",
         "achieved": round(active_tflops, 2),
         "peak": BF16_PEAK_TFLOPS,
@@ -257,7 +267,7 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, args.cpu_heads, t_call_ms, hunyuan)
+        cpu = cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, args.cpu_heads, t_call_ms, hunyuan, ear)
 
     line = {
         "metric": METRIC,
@@ -273,16 +283,17 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded Gaussian mixture with per-frame drift, drawn on device)",
         "config": {
-            "workload": f"{cfg.name}: one SVOO attention call, H={h} N={n} d={d} Qc={qcn} Kc={kcn}, "
-                        f"{iters} warm-started k-means iterations, {args.mode} mask mode",
+            "workload": f"{cfg.name}: one SVOO{'-EAR' if ear else ''} attention call, H={h} N={n} d={d} "
+                        f"Qc={qcn} Kc={kcn}, {iters} warm-started k-means iterations, {args.mode} mask mode",
             "heads": h, "tokens": n, "head_dim": d, "q_clusters": qcn, "k_clusters": kcn,
-            "kmeans_iters": iters, "top_p": top_p, "mask_mode": args.mode,
+            "kmeans_iters": iters, "top_p": top_p, "mask_mode": args.mode, "pattern": args.pattern,
         },
         "latency_ms": round(t_call_ms, 4),
         "reuse_step_ms": round(reuse_ms, 4),
         "stages_ms": {kk: round(vv, 4) for kk, vv in stages_ms.items()},
         "text_tokens": cfg.text_tokens,
         "realized_density": round(realized_density, 5),
+        "centroid_pairs": cent_pairs,
         "active_tflops": round(active_tflops, 2),
         "permute_gbps": round(permute_bytes / (permute_ms * 1e-3) / 1e9, 1),
         "permute_frac_hbm": round(permute_bytes / (permute_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
@@ -618,7 +629,7 @@ def cpu_baseline_dit(model, lat, txt, rho, top_p, dmin, dmax, nheads, t_step_ms,
     }
 
 
-def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms, hunyuan=False):
+def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms, hunyuan=False, ear=False):
     """The numpy oracle on ``nheads`` heads of the same inputs; latency scaled linearly to all heads."""
     import numpy as np
 
@@ -636,6 +647,9 @@ def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms,
         O.hunyuan_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
                                  cfg.text_tokens, cfg.text_tokens, init_q_centroids=qi, init_k_centroids=ki,
                                  attn_dtype=np.float32)
+    elif ear:
+        O.ear_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs, 1.0,
+                             init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
     else:
         O.svoo_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
                               init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
@@ -649,7 +663,8 @@ def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms,
         "cores": cpu_threads(),
         "kind": "port",
         "sample": f"{nheads} of {h} heads of the same inputs, full call (k-means {cfg.kmeans_iters} warm-started "
-                  f"iterations, mask, permutes, fp32 block-sparse attention) in the numpy oracle: {t:.2f} s; "
+                  f"iterations, {'EAR scoring and selection' if ear else 'mask'}, permutes, fp32 "
+                  f"{'compensated ' if ear else ''}block-sparse attention) in the numpy oracle: {t:.2f} s; "
                   f"scaled x{h / nheads:g} to {call_s:.1f} s per call = {call_s * 1e3 / t_call_ms:.0f}x the GPU "
                   f"latency",
         "call_s_scaled": round(call_s, 3),

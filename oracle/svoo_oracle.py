@@ -14,7 +14,12 @@ Rounding contract (applies to the GPU implementation as well)
   storage dtype, where the reference rounds a matmul output.
 * Centroid sums are exact (float64), rounded to float32, divided by the count in
   float32 (IEEE division) and rounded to the storage dtype.
-* Sorting is stable: ties go to the lower original index.
+* Sorting is stable: ties go to the lower original index (-0.0 and +0.0 tie).
+* EAR (error-aware routing): value centroids are the exact member sum rounded to
+  bf16, divided by the bf16-rounded count (the reference's bf16 tensor ops); the
+  efficiency scores are evaluated in float64 (the reference's fp32 expansion is
+  ill-conditioned where a centroid reproduces its block); budget and greedy areas
+  are exact integers (the reference sums them in float32).
 """
 
 from __future__ import annotations

@@ -32,7 +32,7 @@ __global__ void __launch_bounds__(kEarThreads) ear_value_kernel(const uint16_t* 
                                                                 int compute_vc, uint16_t* __restrict__ vc,
                                                                 float* __restrict__ vc_sq,
                                                                 float2* __restrict__ tok_stats) {
-  __shared__ double part[2][128];
+  __shared__ double part[16][128];
   __shared__ float vcs[128];
   const int j = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int lane = tid % kWave, wave = tid / kWave;
@@ -40,14 +40,27 @@ __global__ void __launch_bounds__(kEarThreads) ear_value_kernel(const uint16_t* 
   const int start = koff[cj], cnt = ks[cj];
   const uint16_t* vb = vp + ((size_t)b * n + start) * 128;
   if (compute_vc) {
-    const int d = tid % 128, g = tid / 128;
-    double s = 0.0;
-    for (int t = g; t < cnt; t += 2) s += (double)bf16_to_f32(vb[(size_t)t * 128 + d]);
-    part[g][d] = s;
+    // 16 row groups x 16 chunks of 8 values: 16-byte loads, fp64 sums (exact for bf16 inputs)
+    const int rg = tid / 16, c8 = tid % 16;
+    double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    for (int t = rg; t < cnt; t += 16) {
+      const u32x4_t w = ((const u32x4_t*)(vb + (size_t)t * 128))[c8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += (double)bf16_to_f32((uint16_t)(w[e] & 0xffffu));
+        acc[2 * e + 1] += (double)bf16_to_f32((uint16_t)(w[e] >> 16));
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[rg][8 * c8 + e] = acc[e];
     __syncthreads();
     if (tid < 128) {
+      double sum = 0.0;
+#pragma unroll
+      for (int g = 0; g < 16; ++g) sum += part[g][tid];
+      const int d = tid;
       // bf16 sum (rounded once), divided by the bf16-rounded count, rounded to bf16
-      const float s_st = bf16_round_f32((float)(part[0][d] + part[1][d]));
+      const float s_st = bf16_round_f32((float)sum);
       const float den = bf16_round_f32((float)max(cnt, 1));
       const uint16_t r = f32_to_bf16(s_st / den);
       vc[cj * 128 + d] = r;
@@ -104,6 +117,7 @@ __global__ void __launch_bounds__(kEarThreads) ear_logits_kernel(const uint16_t*
   for (int j = tid; j < kn; j += kEarThreads) {
     const u32x4_t* row = (const u32x4_t*)(kb + (size_t)j * 128);
     double acc = 0.0;
+#pragma unroll 2
     for (int ch = 0; ch < 16; ++ch) {
       const u32x4_t w = row[ch];
 #pragma unroll
@@ -124,10 +138,22 @@ __global__ void __launch_bounds__(kEarThreads) ear_logits_kernel(const uint16_t*
 // permuted (lane half h covers d in [64h, 64h+64), k-step s the 8 values at 64h + 8s) identically
 // in both operands, so every lane loads 128 contiguous bytes of its row.
 constexpr int kEffClusters = 8;
+constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
+
+// expm1(x) for |x| <= 0.1 by its Taylor series to x^4 (truncation below 1e-6 relative); beyond
+// 0.1 the difference e^a - e^c itself loses at most 6e-8 / 0.1 relative in fp32.
+constexpr float kExpm1Lim = 0.1f;
+__device__ __forceinline__ float expm1_small(float x) {
+  float p = fmaf(x, 1.0f / 24.0f, 1.0f / 6.0f);
+  p = fmaf(p, x, 0.5f);
+  p = fmaf(p, x, 1.0f);
+  return p * x;
+}
+
 __global__ void __launch_bounds__(kEarThreads) ear_efficiency_kernel(
     const uint16_t* __restrict__ qc, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ clog,
     const float2* __restrict__ tok_stats, const float* __restrict__ vc_sq, const int32_t* __restrict__ qs,
-    const int32_t* __restrict__ ks, const int32_t* __restrict__ koff, int n, int qn, int kn, float scale,
+    const int32_t* __restrict__ ks, const int32_t* __restrict__ koff, int n, int qn, int kn, float scale2,
     float gamma, float log_eps, float eps, float* __restrict__ eff) {
   const int b = blockIdx.y, j0 = blockIdx.x * kEffClusters;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, h = lane / 32, l32 = lane % 32;
@@ -149,50 +175,58 @@ __global__ void __launch_bounds__(kEarThreads) ear_efficiency_kernel(
       const size_t cj = (size_t)b * kn + j;
       const int start = koff[cj], cnt = ks[cj];
       const float c = bf16_to_f32(crow[j]);
-      // sums of e^2 |u|^2, e d (u . vc) and d^2, all relative to the running max m
-      float m = c, sd = 0.0f, sg = 0.0f, sc = 0.0f;
+      const float c2 = c * kLog2e;
+      // sums of e^2 |u|^2, e d (u . vc) and d^2, relative to the running max m2 (log2 units)
+      float m2 = c2, sd = 0.0f, sg = 0.0f, sc = 0.0f;
       for (int tt = 0; tt < cnt; tt += 32) {
         const int row = min(start + tt + l32, n - 1);
         const u32x4_t* kr = (const u32x4_t*)(kb + (size_t)row * 128) + 8 * h;
+        u32x4_t ka[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) ka[s] = kr[s];
+        // token statistics of this lane's 16 tokens, loaded with the K rows (clamped rows are masked below)
+        float2 sv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sv[r] = st[min(start + tt + (r / 4) * 8 + h * 4 + (r % 4), n - 1)];
         f32x16_t sacc = f32x16_t{};
 #pragma unroll
-        for (int s = 0; s < 8; ++s) sacc = mfma32x32x16(as_bf16x8(kr[s]), as_bf16x8(qop[s]), sacc);
-        float av[16];
+        for (int s = 0; s < 8; ++s) sacc = mfma32x32x16(as_bf16x8(ka[s]), as_bf16x8(qop[s]), sacc);
+        const bool full = tt + 32 <= cnt;  // wave-uniform: no masking inside the cluster
+        float av[16];  // a_t in log2 units
         float tmax = -INFINITY;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int tok = tt + (r / 4) * 8 + h * 4 + (r % 4);
-          av[r] = tok < cnt ? sacc[r] * scale : -INFINITY;
+          av[r] = (full || tok < cnt) ? sacc[r] * scale2 : -INFINITY;
           tmax = fmaxf(tmax, av[r]);
         }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        if (tmax > m) {
-          const float f = expf(m - tmax), f2 = f * f;
+        if (tmax > m2) {
+          const float f = __builtin_amdgcn_exp2f(m2 - tmax), f2 = f * f;
           sd *= f2;
           sg *= f2;
           sc *= f2;
-          m = tmax;
+          m2 = tmax;
         }
-        const float pc = expf(c - m);
+        const float pc = __builtin_amdgcn_exp2f(c2 - m2);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int tok = tt + (r / 4) * 8 + h * 4 + (r % 4);
-          if (tok < cnt) {
-            const float2 sv = st[start + tok];
-            const float e = expf(av[r] - m);
-            const float da = av[r] - c;
-            const float d = fabsf(da) < 0.5f ? pc * expm1f(da) : e - pc;
-            sd = fmaf(e * e, sv.x, sd);
-            sg = fmaf(e * d, sv.y, sg);
-            sc = fmaf(d, d, sc);
-          }
+          const float e = __builtin_amdgcn_exp2f(av[r] - m2);  // 0 for masked tokens
+          const float x = (av[r] - c2) * kLn2;                  // a_t - c_ij
+          float d = fabsf(x) <= kExpm1Lim ? pc * expm1_small(x) : e - pc;
+          if (!full && tok >= cnt) d = 0.0f;
+          sd = fmaf(e * e, sv[r].x, sd);
+          sg = fmaf(e * d, sv[r].y, sg);
+          sc = fmaf(d, d, sc);
         }
       }
       sd += __shfl_xor(sd, 32);
       sg += __shfl_xor(sg, 32);
       sc += __shfl_xor(sc, 32);
       const float err = sd + 2.0f * sg + vc_sq[cj] * sc;
-      const float lerr = fmaxf(err > 0.0f ? logf(err) + 2.0f * m : -INFINITY, log_eps);
+      // log(err) + 2m with m = m2 ln2, via the hardware log2
+      const float lerr = fmaxf(err > 0.0f ? (__builtin_amdgcn_logf(err) + 2.0f * m2) * kLn2 : -INFINITY, log_eps);
       const float area = fmaxf(qsz * (float)cnt, eps);
       if (h == 0 && i < qn) eff[((size_t)b * qn + i) * kn + j] = lerr - gamma * logf(area);
     }
@@ -404,10 +438,10 @@ extern "C" int svoo_ear_efficiency(const uint16_t* qc, const uint16_t* k_perm, c
   SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_ear_efficiency: D=%d (only 128 supported)", d);
   SVOO_REQUIRE(bh > 0 && n > 0 && qn > 0 && kn > 0 && bh <= 65535 && eps > 0.0f, SVOO_ERR_INVALID_ARG,
                "svoo_ear_efficiency: bad dims");
-  const float scale = 1.0f / (float)sqrt((double)d);
+  const float scale2 = (float)(1.4426950408889634 / sqrt((double)d));  // log2(e) / sqrt(D)
   dim3 grid((kn + kEffClusters - 1) / kEffClusters, bh);
   hipLaunchKernelGGL(ear_efficiency_kernel, grid, dim3(kEarThreads), 0, (hipStream_t)stream, qc, k_perm, c_logits,
-                     (const float2*)tok_stats, vc_sq, q_sizes, k_sizes, k_offsets, n, qn, kn, scale, gamma,
+                     (const float2*)tok_stats, vc_sq, q_sizes, k_sizes, k_offsets, n, qn, kn, scale2, gamma,
                      logf(eps), eps, eff);
   return check_launch("svoo_ear_efficiency");
 }

@@ -252,8 +252,14 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   const uint16_t* kb = k + head;
   const uint16_t* vb = v + head;
   uint16_t* ob = o + head;
-  const uint16_t* kcb = EAR ? kc + (size_t)b * kn * 128 : nullptr;
-  const uint16_t* vcb = EAR ? vc + (size_t)b * kn * 128 : nullptr;
+  // EAR: the centroid rows are addressed from the token base of the head, as rows at a signed offset
+  // (the host checks that the buffers are 256-byte congruent and that every row index fits int32), so
+  // the DMA path is the same as for token rows.
+  int crow_k = 0, crow_v = 0;
+  if constexpr (EAR) {
+    crow_k = (int)(((long long)(uintptr_t)(kc + (size_t)b * kn * 128) - (long long)(uintptr_t)kb) / 256);
+    crow_v = (int)(((long long)(uintptr_t)(vc + (size_t)b * kn * 128) - (long long)(uintptr_t)vb) / 256);
+  }
 
   int32_t* seg_start = seg_mem;
   int32_t* seg_cum = seg_mem + kn;
@@ -297,28 +303,28 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
 
   // Row tables: wave 4 resolves K tiles, wave 5 V tiles (lane = tile position).
   // Rows past the stream repeat its last token row (0 when an EAR row has no active tokens); EAR
-  // centroid j is entered as row -1 - j.
+  // centroid j of the K (V) table is row crow_k + j (crow_v + j).
   const int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
   KvCursor cursor;
   if ((wave == 4 || wave == 5) && nseg > 0) cursor_init(cursor, seg_start, seg_cum, nseg, min(lane, total_tok - 1));
+  const int crow = wave == 4 ? crow_k : crow_v;  // the resolving waves: 4 for K, 5 for V
   auto resolve = [&](int32_t* tab, int t) {
     const int p = t * kKT + lane;
     if (p < total_tok)
       tab[lane] = cursor_row(cursor, seg_start, seg_cum, p);
     else if (EAR && p < total)
-      tab[lane] = -1 - cent_idx[p - total_tok];
+      tab[lane] = crow + cent_idx[p - total_tok];
     else
       tab[lane] = last_row;
   };
   // DMA mapping (group B): wave 4+w, group j moves tile rows 4(kDmaIt w + j) + lane/16.
   const int prow = lane / 16, pch = lane % 16;
-  auto dma = [&](const uint16_t* src, const uint16_t* csrc, const int32_t* tab, uint16_t* buf) {
+  auto dma = [&](const uint16_t* src, const int32_t* tab, uint16_t* buf) {
 #pragma unroll
     for (int j = 0; j < kDmaIt; ++j) {
       const int r = 4 * (kDmaIt * wg + j) + prow;
-      const int tr = tab[r];
-      const uint16_t* rp = (EAR && tr < 0) ? csrc + (size_t)(-1 - tr) * 128 : src + (size_t)tr * 128;
-      lds_dma16(rp + swz(r, pch) * 8, buf + 4 * (kDmaIt * wg + j) * 128);
+      const long long row = tab[r];  // negative for EAR centroid rows below the token buffer
+      lds_dma16(src + row * 128 + swz(r, pch) * 8, buf + 4 * (kDmaIt * wg + j) * 128);
     }
   };
 
@@ -436,8 +442,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   };
   // Group B housekeeping at the start of its V(t): DMA K(t+2), V(t+1); resolve K(t+3), V(t+2).
   auto fetch = [&](int t, uint16_t* kdst, uint16_t* vdst) {
-    if (t + 2 < ntiles) dma(kb, kcb, rowtab[0][t & 1], kdst);
-    if (t + 1 < ntiles) dma(vb, vcb, rowtab[1][(t + 1) & 1], vdst);
+    if (t + 2 < ntiles) dma(kb, rowtab[0][t & 1], kdst);
+    if (t + 1 < ntiles) dma(vb, rowtab[1][(t + 1) & 1], vdst);
     if (wave == 4 && t + 3 < ntiles) resolve(rowtab[0][(t + 1) & 1], t + 3);
     if (wave == 5 && t + 2 < ntiles) resolve(rowtab[1][t & 1], t + 2);
   };
@@ -454,9 +460,9 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   }
   __syncthreads();
   if (group_b) {
-    dma(kb, kcb, rowtab[0][0], k_s0);
-    dma(vb, vcb, rowtab[1][0], v_s0);
-    if (ntiles > 1) dma(kb, kcb, rowtab[0][1], k_s1);
+    dma(kb, rowtab[0][0], k_s0);
+    dma(vb, rowtab[1][0], v_s0);
+    if (ntiles > 1) dma(kb, rowtab[0][1], k_s1);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   __syncthreads();
@@ -598,6 +604,16 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   SVOO_REQUIRE(lay.cap < 65536, SVOO_ERR_UNSUPPORTED, "%s: too many q tiles per head", name);
   SVOO_REQUIRE(workspace && ws_bytes >= lay.total, SVOO_ERR_WORKSPACE, "%s: workspace %zu < %zu", name, ws_bytes,
                lay.total);
+  if (EAR) {
+    // centroid rows are addressed as signed int32 row offsets from the token buffers
+    const long long dk = (long long)(uintptr_t)kc - (long long)(uintptr_t)k;
+    const long long dv = (long long)(uintptr_t)vc - (long long)(uintptr_t)v;
+    SVOO_REQUIRE(dk % 256 == 0 && dv % 256 == 0, SVOO_ERR_INVALID_ARG,
+                 "%s: centroid buffers must be 256-byte congruent with k and v", name);
+    const long long lim = (1ll << 31) - 1 - (long long)bh * (s + kn);
+    SVOO_REQUIRE(llabs(dk / 256) < lim && llabs(dv / 256) < lim, SVOO_ERR_UNSUPPORTED,
+                 "%s: centroid buffers too far from k / v for int32 row offsets", name);
+  }
   hipStream_t st = (hipStream_t)stream;
   char* base = (char*)workspace;
   int32_t* qoff = (int32_t*)(base + lay.qoff);

@@ -4,6 +4,18 @@ The reference ships no test, golden vector or known-answer test for this path, s
 function is pinned by what the mathematics fixes: brute force from the definition on tiny inputs,
 hand-worked selections, and closed forms (dense attention where nothing is pruned, exact
 compensation where every pruned cluster is a point mass at its centroid).
+
+Pinning map (oracle function -> independent checks):
+  value_centroids             small-integer means; empty cluster -> 0; the bf16 count rounding (301 -> 300)
+  value_stats                 per-token dot products in float64
+  ear_centroid_logits         exact small-integer dots times float32(D**-0.5)
+  ear_efficiency_scores       brute force from the vector-norm definition (no expansion), gamma 0 / 0.5 / 1;
+                              empty cluster; logits of 100 stay finite (log err = 200)
+  ear_row_params              scalar / per-head / length-1 / other-length branches; float32 reads
+  ear_select                  hand-worked budgets and greedy fills; ties by index; random invariants
+  ear_compensated_attention   all-active map = dense attention; all-inactive = centroid attention with the
+                              log|K| prior; point-mass clusters = dense attention for any map
+  ear_attention_call          min ratio 1 keeps every block: the call equals dense attention
 """
 
 import numpy as np
