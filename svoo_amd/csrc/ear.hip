@@ -200,7 +200,7 @@ __global__ void __launch_bounds__(kEarThreads) ear_efficiency_kernel(
           av[r] = (full || tok < cnt) ? sacc[r] * scale2 : -INFINITY;
           tmax = fmaxf(tmax, av[r]);
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        tmax = xhalf_max(tmax);
         if (tmax > m2) {
           const float f = __builtin_amdgcn_exp2f(m2 - tmax), f2 = f * f;
           sd *= f2;
@@ -221,9 +221,9 @@ __global__ void __launch_bounds__(kEarThreads) ear_efficiency_kernel(
           sc = fmaf(d, d, sc);
         }
       }
-      sd += __shfl_xor(sd, 32);
-      sg += __shfl_xor(sg, 32);
-      sc += __shfl_xor(sc, 32);
+      sd = xhalf_sum(sd);
+      sg = xhalf_sum(sg);
+      sc = xhalf_sum(sc);
       const float err = sd + 2.0f * sg + vc_sq[cj] * sc;
       // log(err) + 2m with m = m2 ln2, via the hardware log2
       const float lerr = fmaxf(err > 0.0f ? (__builtin_amdgcn_logf(err) + 2.0f * m2) * kLn2 : -INFINITY, log_eps);

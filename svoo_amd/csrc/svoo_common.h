@@ -80,6 +80,19 @@ __device__ __forceinline__ void lds_dma16(const void* src, uint16_t* lds_base) {
                                    (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
+// Max / sum of a value and its partner lane (lane ^ 32), in both lanes: one v_permlane32_swap (a VALU
+// op) instead of a ds_bpermute round trip through LDS.  The swap returns {lanes 0-31 of the first operand
+// with lanes 0-31 of the second in the upper half, lanes 32-63 of the first in the lower half with lanes
+// 32-63 of the second}; with both operands x, each lane sees x of itself and of its partner.
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---------------------------------------------------------------- block reductions
 template <int kThreads>
 __device__ __forceinline__ double block_sum_f64(double v, double* scratch) {

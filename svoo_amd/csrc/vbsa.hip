@@ -357,22 +357,52 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       }
     }
   };
-  // MFMA phase M(t): O += V(t)^T P(t)^T, then S(t+1) (if any).
-  auto mphase = [&](int t, const uint16_t* vt, const uint16_t* knext) {
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const int rb = (kb2 * 32 + st * 16) * 128;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-          const uint2 lo = ds_read_tr16_b64(&vt[rb + voffs[0][db]]);
-          const uint2 hi = ds_read_tr16_b64(&vt[rb + voffs[1][db]]);
-          acc[db] = mfma32x32x16(as_bf16x8(u32x4_t{lo.x, lo.y, hi.x, hi.y}), as_bf16x8(pop[kb2][st]), acc[db]);
-        }
-      }
+  // MFMA phase M(t): O += V(t)^T P(t)^T, then S(t+1).  The 32 MFMAs run as one software pipeline whose
+  // operand reads are issued two MFMAs ahead into three rotating buffers (the order is pinned with
+  // scheduling barriers).  S(t+1) is also computed after the last tile, on stale LDS, and not used.
+  auto mop = [&](int i, const uint16_t* vt, const uint16_t* knext) -> u32x4_t {
+    if (i < 16) {
+      const int kb2 = i / 8, st = (i / 4) % 2, db = i % 4;
+      const int rb = (kb2 * 32 + st * 16) * 128;
+      const uint2 lo = ds_read_tr16_b64(&vt[rb + voffs[0][db]]);
+      const uint2 hi = ds_read_tr16_b64(&vt[rb + voffs[1][db]]);
+      return u32x4_t{lo.x, lo.y, hi.x, hi.y};
     }
-    if (t + 1 < ntiles) scores(knext);
+    const int j = i - 16, ks2 = j / 2, kb2 = j % 2;
+    return *(const u32x4_t*)(&knext[kb2 * 32 * 128 + koffs[ks2]]);
+  };
+  auto mphase = [&](int t, const uint16_t* vt, const uint16_t* knext) {
+    u32x4_t buf[3];
+    buf[0] = mop(0, vt, knext);
+    buf[1] = mop(1, vt, knext);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    auto mm = [&](int i) {
+      if (i < 16) {
+        const int kb2 = i / 8, st = (i / 4) % 2, db = i % 4;
+        acc[db] = mfma32x32x16(as_bf16x8(buf[i % 3]), as_bf16x8(pop[kb2][st]), acc[db]);
+      } else {
+        const int j = i - 16, ks2 = j / 2, kb2 = j % 2;
+        if (j < 2) sacc[kb2] = f32x16_t{};
+        sacc[kb2] = mfma32x32x16(as_bf16x8(buf[i % 3]), as_bf16x8(qop[ks2]), sacc[kb2]);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+      buf[(i + 2) % 3] = mop(i + 2, vt, knext);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      mm(i);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+#pragma unroll
+    for (int i = 14; i < 30; ++i) {
+      buf[(i + 2) % 3] = mop(i + 2, vt, knext);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      mm(i);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    mm(30);
+    mm(31);
+    (void)t;
   };
   // VALU phase V(t): online softmax of S(t) -> bf16 P(t) (per lane: one query, 32 of 64 keys).
   auto vphase = [&](int t) {
@@ -412,7 +442,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb2][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * sl;
+    mx = xhalf_max(mx) * sl;
     if (__any(mx > m_run + 8.0f)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -424,21 +454,27 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
         for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
     }
     const float mneg = -m_run;
-    float ls = 0.0f;
+    // The row sum adds the bf16 P pairs the PV MFMA consumes, two per v_dot2 with (1, 1).
+    const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+    float ls0 = 0.0f, ls1 = 0.0f;
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
       float pv[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][r], sl, mneg));
-        ls += pv[r];
-      }
+      for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][r], sl, mneg));
 #pragma unroll
       for (int st = 0; st < 2; ++st)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pop[kb2][st][e] = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
+          pop[kb2][st][e] = w;
+          if (e & 1)
+            ls1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, ls1, false);
+          else
+            ls0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, ls0, false);
+        }
     }
-    l_run += ls;
+    l_run += ls0 + ls1;
   };
   // Group B housekeeping at the start of its V(t): DMA K(t+2), V(t+1); resolve K(t+3), V(t+2).
   auto fetch = [&](int t, uint16_t* kdst, uint16_t* vdst) {
@@ -509,7 +545,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
 
   if (!active) return;
   // Normalise and store: lane holds d = db*32 + (r/4)*8 + 4h + r%4 of query l32.
-  const float lt = l_run + __shfl_xor(l_run, 32);
+  const float lt = xhalf_sum(l_run);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   const int row = qrow0 + l32;
   if (row < q1) {
