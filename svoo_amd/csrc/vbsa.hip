@@ -320,11 +320,20 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   // DMA mapping (group B): wave 4+w, group j moves tile rows 4(kDmaIt w + j) + lane/16.
   const int prow = lane / 16, pch = lane % 16;
   auto dma = [&](const uint16_t* src, const int32_t* tab, uint16_t* buf) {
+    int rows[kDmaIt];  // all table reads first: one LDS wait for the group
+#pragma unroll
+    for (int j = 0; j < kDmaIt; ++j) rows[j] = tab[4 * (kDmaIt * wg + j) + prow];
 #pragma unroll
     for (int j = 0; j < kDmaIt; ++j) {
       const int r = 4 * (kDmaIt * wg + j) + prow;
-      const long long row = tab[r];  // negative for EAR centroid rows below the token buffer
-      lds_dma16(src + row * 128 + swz(r, pch) * 8, buf + 4 * (kDmaIt * wg + j) * 128);
+      if constexpr (EAR) {
+        // negative rows for EAR centroid rows below the token buffer
+        lds_dma16(src + (long long)rows[j] * 128 + swz(r, pch) * 8, buf + 4 * (kDmaIt * wg + j) * 128);
+      } else {
+        // a head's rows are < 2^24: a 32-bit byte offset from the wave-uniform base (SGPR-based addressing)
+        const uint32_t off = (uint32_t)rows[j] * 256u + (uint32_t)swz(r, pch) * 16u;
+        lds_dma16((const char*)src + off, buf + 4 * (kDmaIt * wg + j) * 128);
+      }
     }
   };
 
@@ -636,6 +645,7 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   SVOO_REQUIRE(bh > 0 && s > 0 && qn > 0 && kn > 0, SVOO_ERR_INVALID_ARG, "%s: bad dims", name);
   SVOO_REQUIRE(kn <= kMaxKN && qn < 32768, SVOO_ERR_UNSUPPORTED, "%s: qn=%d kn=%d above limits", name, qn, kn);
   SVOO_REQUIRE((long long)bh * s * 128 < (1ll << 40), SVOO_ERR_UNSUPPORTED, "%s: too large", name);
+  SVOO_REQUIRE(s < (1 << 24), SVOO_ERR_UNSUPPORTED, "%s: S=%d above 2^24 tokens per head", name, s);
   const VbsaWs lay = vbsa_layout(bh, s, qn, kn);
   SVOO_REQUIRE(lay.cap < 65536, SVOO_ERR_UNSUPPORTED, "%s: too many q tiles per head", name);
   SVOO_REQUIRE(workspace && ws_bytes >= lay.total, SVOO_ERR_WORKSPACE, "%s: workspace %zu < %zu", name, ws_bytes,
