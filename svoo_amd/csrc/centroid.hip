@@ -7,7 +7,10 @@
 //   not depend on the order of the atomics.  The wave's indices and labels arrive in two vector
 //   loads; rows are then fetched 16 at a time, one batch ahead of the accumulation.
 // finalize: centroid = bf16(f32(sum) / f32(size)), size 0 keeps the old centroid; the sum buffer
-//   is cleared on the way out so the next update starts from zero.
+//   is cleared on the way out so the next update starts from zero (or kept, for the delta update).
+// delta: the co-clustering's later iterations move only the rows whose label changed: one wave per
+//   listed token subtracts its row from the old cluster's sums and adds it to the new one's (fp64
+//   atomics; exact, so the sums equal a full recount) and moves one count.
 #include "svoo_common.h"
 
 namespace svoo {
@@ -83,13 +86,15 @@ __global__ void __launch_bounds__(256) centroid_accumulate_kernel(const uint32_t
 __global__ void __launch_bounds__(256) centroid_finalize_kernel(double* __restrict__ sums,
                                                                 const int32_t* __restrict__ sizes,
                                                                 const uint16_t* old_c, uint16_t* new_c,
-                                                                long long total, int d) {
+                                                                long long total, int d, int keep_sums,
+                                                                int32_t* __restrict__ reset) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (reset && i == 0) *reset = 0;  // the delta list's counter, consumed by now
   if (i >= total) return;
   const long long row = i / d;
   const int cnt = sizes[row];
   const double s = sums[i];
-  sums[i] = 0.0;
+  if (!keep_sums) sums[i] = 0.0;
   if (cnt > 0) {
     const float mean = (float)s / (float)cnt;
     new_c[i] = f32_to_bf16(mean);
@@ -103,6 +108,39 @@ __global__ void zero_f64_kernel(double* __restrict__ p, long long n) {
   if (i < n) p[i] = 0.0;
 }
 
+__global__ void zero_i32_kernel(int32_t* __restrict__ p, long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+constexpr int kDeltaBlocks = 1024;  // grid-stride over the change list (its length is on the device)
+__global__ void __launch_bounds__(256) centroid_delta_kernel(const uint32_t* __restrict__ x,
+                                                             const int2* __restrict__ changes,
+                                                             const int32_t* __restrict__ nchanges,
+                                                             double* __restrict__ sums, int32_t* __restrict__ sizes,
+                                                             int n, int k) {
+  const int lane = threadIdx.x % kWave;
+  const int w0 = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int nw = gridDim.x * (blockDim.x / kWave);
+  const int total = *nchanges;
+  for (int e = w0; e < total; e += nw) {
+    const int2 c = changes[e];
+    const int b = c.x / n, ol = c.y >> 16, nl = c.y & 0xffff;
+    const uint32_t w = x[(size_t)c.x * 64 + lane];
+    const double v0 = (double)bf16_to_f32((uint16_t)(w & 0xffffu)), v1 = (double)bf16_to_f32((uint16_t)(w >> 16));
+    double* sn = sums + ((size_t)b * k + nl) * 128 + 2 * lane;
+    double* so = sums + ((size_t)b * k + ol) * 128 + 2 * lane;
+    atomicAdd(sn, v0);
+    atomicAdd(sn + 1, v1);
+    atomicAdd(so, -v0);
+    atomicAdd(so + 1, -v1);
+    if (lane == 0) {
+      atomicAdd(&sizes[(size_t)b * k + nl], 1);
+      atomicAdd(&sizes[(size_t)b * k + ol], -1);
+    }
+  }
+}
+
 }  // namespace svoo
 
 using namespace svoo;
@@ -113,10 +151,29 @@ int svoo_zero_f64(double* p, long long n, hipStream_t stream) {
   return check_launch("zero_f64");
 }
 
-// sums must be zero on entry; it is zero again on return.
+int svoo_zero_i32(int32_t* p, long long n, hipStream_t stream) {
+  if (n <= 0) return SVOO_OK;
+  hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, n);
+  return check_launch("zero_i32");
+}
+
+// Moves the listed tokens between the (kept) fp64 sums and counts, then recomputes the centroids;
+// *reset (the list's counter) is cleared by the finalize.
+int svoo_centroid_delta_impl(const uint16_t* x, const int2* changes, const int32_t* nchanges, double* sums,
+                             int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
+                             int32_t* reset, hipStream_t stream) {
+  hipLaunchKernelGGL(centroid_delta_kernel, dim3(kDeltaBlocks), dim3(256), 0, stream, (const uint32_t*)x, changes,
+                     nchanges, sums, sizes, n, k);
+  const long long total = (long long)bh * k * 128;
+  hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, sums,
+                     sizes, old_c, new_c, total, 128, 1, reset);
+  return check_launch("svoo_centroid_delta");
+}
+
+// sums must be zero on entry; it is zero again on return unless keep_sums.
 int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
                               const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
-                              double* sums, hipStream_t stream) {
+                              double* sums, hipStream_t stream, int keep_sums) {
   const int waves_per_block = 4;
   const int pos_per_block = waves_per_block * kCentPosPerWave;
   dim3 grid((n + pos_per_block - 1) / pos_per_block, bh);
@@ -124,7 +181,7 @@ int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, cons
                      sorted_labels, sums, n, k);
   const long long total = (long long)bh * k * 128;
   hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, sums,
-                     sizes, old_c, new_c, total, 128);
+                     sizes, old_c, new_c, total, 128, keep_sums, (int32_t*)nullptr);
   return check_launch("svoo_centroid_update");
 }
 
@@ -147,5 +204,5 @@ extern "C" int svoo_centroid_update(const uint16_t* x, const int32_t* sorted_idx
   hipStream_t s = (hipStream_t)stream;
   double* sums = (double*)workspace;
   if (int rc = svoo_zero_f64(sums, (long long)bh * k * d, s)) return rc;
-  return svoo_centroid_update_impl(x, sorted_idx, sorted_labels, sizes, old_c, new_c, bh, n, k, sums, s);
+  return svoo_centroid_update_impl(x, sorted_idx, sorted_labels, sizes, old_c, new_c, bh, n, k, sums, s, 0);
 }

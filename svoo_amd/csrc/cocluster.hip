@@ -10,6 +10,8 @@
 // assign: 4 waves x 128 tokens per block; token rows stay in registers as the MFMA B operand,
 //         E streams through LDS in 64-row chunks (hi and lo, double buffered, LDS DMA), and each
 //         lane keeps a running argmax over the 16 cluster rows it holds of every 32x32 tile.
+//         From the second iteration on it also lists the tokens whose label changed, and the
+//         centroid sums are updated from that list alone (exact fp64, so equal to a full recount).
 #include "svoo_common.h"
 
 namespace svoo {
@@ -135,7 +137,8 @@ constexpr int kAsgTok = 4 * kAsgTokWave;
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi,
-                        const uint16_t* __restrict__ e_lo, int32_t* __restrict__ labels, int n, int j, int jpad) {
+                        const uint16_t* __restrict__ e_lo, int32_t* __restrict__ labels, int n, int j, int jpad,
+                        int2* __restrict__ changes, int32_t* __restrict__ nchanges) {
   __shared__ __attribute__((aligned(16))) uint16_t s_e[2][2][kAssignChunk * 128];  // [buffer][hi, lo]
   const int bidx = blockIdx.y;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -233,7 +236,15 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
     }
     const int tok = tok0 + cb * 32 + l32;
     // padding rows repeat row j - 1: a padding winner stands for row j - 1
-    if (h == 0 && tok < n) labels[(size_t)bidx * n + tok] = min(best_j[cb], j - 1);
+    if (h == 0 && tok < n) {
+      const int nl = min(best_j[cb], j - 1);
+      int32_t* lp = labels + (size_t)bidx * n + tok;
+      if (nchanges) {  // labels holds the previous iteration's labels: list the changes
+        const int ol = *lp;
+        if (ol != nl) changes[atomicAdd(nchanges, 1)] = make_int2(bidx * n + tok, (ol << 16) | nl);
+      }
+      *lp = nl;
+    }
   }
 }
 
@@ -247,7 +258,11 @@ int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t*
                            hipStream_t stream);
 int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
                               const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
-                              double* sums, hipStream_t stream);
+                              double* sums, hipStream_t stream, int keep_sums = 0);
+int svoo_centroid_delta_impl(const uint16_t* x, const int2* changes, const int32_t* nchanges, double* sums,
+                             int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
+                             int32_t* reset, hipStream_t stream);
+int svoo_zero_i32(int32_t* p, long long n, hipStream_t stream);
 int svoo_zero_f64(double* p, long long n, hipStream_t stream);
 
 static inline int pad_to(int v, int m) { return (v + m - 1) / m * m; }
@@ -270,9 +285,10 @@ static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uin
 }
 
 static int assign_launch(const uint16_t* x, const uint16_t* e_hi, const uint16_t* e_lo, int32_t* labels, int bh, int n,
-                         int j, int jpad, hipStream_t stream) {
+                         int j, int jpad, hipStream_t stream, int2* changes = nullptr, int32_t* nchanges = nullptr) {
   dim3 grid((n + kAsgTok - 1) / kAsgTok, bh);
-  hipLaunchKernelGGL(cocluster_assign_kernel, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad);
+  hipLaunchKernelGGL(cocluster_assign_kernel, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad, changes,
+                     nchanges);
   return check_launch("svoo_cocluster_assign");
 }
 
@@ -303,10 +319,13 @@ extern "C" int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, co
 // Workspace layout of svoo_co_cluster (each region 256-byte aligned):
 //   e_hi, e_lo   [bh][jpad_max][128] bf16
 //   counts       [bh][kmax][nchunks] int32   (cluster-sort scratch)
-//   sums         [bh][kmax][128] fp64        (centroid sums, kept zero between uses)
+//   sums_k       [bh][kc][128] fp64          (key-centroid sums, kept across iterations)
 //   sorted_lab   [bh][n] int32
+//   sums_q       [bh][qc][128] fp64          (query-centroid sums)
+//   changes      [bh * n] int2               (label changes of one assignment: token, old << 16 | new)
+//   nchanges     2 int32                     (change counters, key and query side)
 struct CoClusterWs {
-  size_t e_off, counts_off, sums_off, slab_off, total;
+  size_t e_off, counts_off, sums_off, slab_off, sums_q_off, changes_off, nchanges_off, total;
 };
 
 static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
@@ -319,8 +338,11 @@ static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
   size_t e_bytes = al((size_t)bh * jpad * 128 * sizeof(uint16_t));
   w.counts_off = 2 * e_bytes;
   w.sums_off = w.counts_off + al((size_t)bh * kmax * nch * sizeof(int32_t));
-  w.slab_off = w.sums_off + al((size_t)bh * kmax * 128 * sizeof(double));
-  w.total = w.slab_off + al((size_t)bh * n * sizeof(int32_t));
+  w.slab_off = w.sums_off + al((size_t)bh * kc * 128 * sizeof(double));
+  w.sums_q_off = w.slab_off + al((size_t)bh * n * sizeof(int32_t));
+  w.changes_off = w.sums_q_off + al((size_t)bh * qc * 128 * sizeof(double));
+  w.nchanges_off = w.changes_off + al((size_t)bh * n * sizeof(int2));
+  w.total = w.nchanges_off + 256;
   return w;
 }
 
@@ -344,7 +366,8 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   SVOO_REQUIRE(qc <= kMaxClusters && kc <= kMaxClusters, SVOO_ERR_UNSUPPORTED,
                "svoo_co_cluster: cluster counts above %d", kMaxClusters);
   SVOO_REQUIRE(max_iters >= 1, SVOO_ERR_INVALID_ARG, "svoo_co_cluster: max_iters=%d must be >= 1", max_iters);
-  SVOO_REQUIRE((long long)bh * n * 128 < (1ll << 40), SVOO_ERR_UNSUPPORTED, "svoo_co_cluster: too large");
+  SVOO_REQUIRE((long long)bh * n * 128 < (1ll << 40) && (long long)bh * n < (1ll << 31), SVOO_ERR_UNSUPPORTED,
+               "svoo_co_cluster: too large");
   const CoClusterWs lay = co_cluster_layout(bh, n, qc, kc);
   SVOO_REQUIRE(workspace && ws_bytes >= lay.total, SVOO_ERR_WORKSPACE, "svoo_co_cluster: workspace %zu < %zu",
                ws_bytes, lay.total);
@@ -354,24 +377,44 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   uint16_t* e_hi = (uint16_t*)(base + lay.e_off);
   uint16_t* e_lo = (uint16_t*)(base + lay.e_off + e_bytes);
   int32_t* counts = (int32_t*)(base + lay.counts_off);
-  double* sums = (double*)(base + lay.sums_off);
+  double* sums_k = (double*)(base + lay.sums_off);
+  double* sums_q = (double*)(base + lay.sums_q_off);
   int32_t* slab = (int32_t*)(base + lay.slab_off);
-  const int kmax = qc > kc ? qc : kc;
+  int2* changes = (int2*)(base + lay.changes_off);
+  int32_t* nch = (int32_t*)(base + lay.nchanges_off);
   const int jpad_k = pad_to(kc, kAssignChunk), jpad_q = pad_to(qc, kAssignChunk);
-  int rc = svoo_zero_f64(sums, (long long)bh * kmax * 128, s);
+  int rc = svoo_zero_f64(sums_k, (long long)bh * kc * 128, s);
+  if (!rc) rc = svoo_zero_f64(sums_q, (long long)bh * qc * 128, s);
+  if (!rc) rc = svoo_zero_i32(nch, 2, s);
+  // One side of an iteration: profiles of x's tokens live in the other side's centroid space.
+  // The first iteration sorts the labels and sums every cluster; later ones list the tokens whose
+  // label changed and move only their rows between the fp64 sums (the finalize resets the counter).
+  auto side = [&](const uint16_t* x, uint16_t* cent, const uint16_t* other, int32_t* labels, int32_t* sizes,
+                  int32_t* sorted_idx, int32_t* offsets, double* sums, int kx, int ko, int jpad, int32_t* cnt,
+                  bool first) -> int {
+    int r;
+    if ((r = prep_launch(cent, other, e_hi, e_lo, nullptr, bh, kx, ko, jpad, s))) return r;
+    if (first) {
+      if ((r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s))) return r;
+      if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, slab, counts, nullptr, s)))
+        return r;
+      return svoo_centroid_update_impl(x, sorted_idx, slab, sizes, cent, cent, bh, n, kx, sums, s, 1);
+    }
+    if ((r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s, changes, cnt))) return r;
+    return svoo_centroid_delta_impl(x, changes, cnt, sums, sizes, cent, cent, bh, n, kx, cnt, s);
+  };
   for (int it = 0; it < max_iters && rc == SVOO_OK; ++it) {
-    // Key step: profiles of keys live in query-centroid space.
-    if ((rc = prep_launch(k_cent, q_cent, e_hi, e_lo, nullptr, bh, kc, qc, jpad_k, s))) break;
-    if ((rc = assign_launch(k, e_hi, e_lo, k_labels, bh, n, kc, jpad_k, s))) break;
-    if ((rc = svoo_cluster_sort_impl(k_labels, bh, n, kc, k_sorted_idx, k_sizes, k_offsets, slab, counts, nullptr, s)))
+    if ((rc = side(k, k_cent, q_cent, k_labels, k_sizes, k_sorted_idx, k_offsets, sums_k, kc, qc, jpad_k, nch,
+                   it == 0)))
       break;
-    if ((rc = svoo_centroid_update_impl(k, k_sorted_idx, slab, k_sizes, k_cent, k_cent, bh, n, kc, sums, s))) break;
-    // Query step: profiles of queries live in the space of the new key centroids.
-    if ((rc = prep_launch(q_cent, k_cent, e_hi, e_lo, nullptr, bh, qc, kc, jpad_q, s))) break;
-    if ((rc = assign_launch(q, e_hi, e_lo, q_labels, bh, n, qc, jpad_q, s))) break;
-    if ((rc = svoo_cluster_sort_impl(q_labels, bh, n, qc, q_sorted_idx, q_sizes, q_offsets, slab, counts, nullptr, s)))
+    if ((rc = side(q, q_cent, k_cent, q_labels, q_sizes, q_sorted_idx, q_offsets, sums_q, qc, kc, jpad_q, nch + 1,
+                   it == 0)))
       break;
-    if ((rc = svoo_centroid_update_impl(q, q_sorted_idx, slab, q_sizes, q_cent, q_cent, bh, n, qc, sums, s))) break;
+  }
+  // The stable sort of the final labels (the first iteration's sort already is when max_iters == 1).
+  if (rc == SVOO_OK && max_iters > 1) {
+    rc = svoo_cluster_sort_impl(k_labels, bh, n, kc, k_sorted_idx, k_sizes, k_offsets, slab, counts, nullptr, s);
+    if (!rc) rc = svoo_cluster_sort_impl(q_labels, bh, n, qc, q_sorted_idx, q_sizes, q_offsets, slab, counts, nullptr, s);
   }
   return rc;
 }
