@@ -213,6 +213,9 @@ int svoo_exact_sparsity_counts(const uint16_t* scores, long long rows, int n, fl
  * layouts the kernels assume.
  * ------------------------------------------------------------------------------------------- */
 int svoo_probe_mfma_layout(float* out32, float* out16, void* stream);
+/* Diagnostic (no reference counterpart): the same for v_mfma_f64_16x16x4_f64 (out: 64 lanes x 4 doubles,
+ * D[i][j] = 64 i + j by the assumed operand layout). */
+int svoo_probe_mfma_f64_layout(double* out, void* stream);
 
 #ifdef __cplusplus
 }

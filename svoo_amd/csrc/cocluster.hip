@@ -126,6 +126,133 @@ __global__ void __launch_bounds__(256) cocluster_prep_kernel(const uint16_t* __r
   }
 }
 
+// --------------------------------------------------------------------------------------- prep (fp64 MFMA)
+// The same three phases for 16 rows of A per block on v_mfma_f64_16x16x4_f64, for profile widths up
+// to kPmMaxKp.  Products of bf16 values are exact in fp64 and the sums are exact as well (the same
+// assumption as the vector kernel), so the results are bit-identical to it whatever the order.
+//   phase 1: praw = bf16(A B^T) tile by tile (16 columns per MFMA tile, the waves take every 4th
+//            tile); the contraction is permuted so that lane quarter q covers d in [32q, 32q+32)
+//            and every lane loads 64 contiguous bytes of its A and B rows;
+//   phase 2: row norms of praw (kept in LDS as bf16, which it is exactly);
+//   phase 3: E = inv * praw B, with B staged through LDS in 64-row chunks (144-element rows, so the
+//            four lane quarters read distinct banks); wave w computes columns [32w, 32w+32).
+constexpr int kPmRows = 16;
+constexpr int kPmChunk = 64;
+constexpr int kPmChunkStride = 144;
+constexpr int kPmMaxKp = 1408;
+
+static inline __host__ __device__ int pm_kpp(int kp) { return (kp + kPmChunk - 1) / kPmChunk * kPmChunk; }
+static inline __host__ __device__ size_t pm_praw_bytes(int kp) {
+  return ((size_t)kPmRows * (pm_kpp(kp) + 2) * sizeof(uint16_t) + 15) / 16 * 16;
+}
+static inline size_t pm_smem(int kp) {
+  return pm_praw_bytes(kp) + kPmRows * sizeof(double) + (size_t)kPmChunk * kPmChunkStride * sizeof(uint16_t);
+}
+
+__device__ __forceinline__ double bf16_half_f64(uint32_t w, int hi) {
+  return (double)bf16_to_f32((uint16_t)(hi ? (w >> 16) : (w & 0xffffu)));
+}
+
+__global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t* __restrict__ a,
+                                                                  const uint16_t* __restrict__ bmat,
+                                                                  uint16_t* __restrict__ e_hi,
+                                                                  uint16_t* __restrict__ e_lo,
+                                                                  float* __restrict__ profile, int j, int kp,
+                                                                  int jpad) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int kpp = pm_kpp(kp), ps = kpp + 2;
+  uint16_t* praw = (uint16_t*)smem;                             // [16][ps] bf16
+  double* inv = (double*)(smem + pm_praw_bytes(kp));           // [16]
+  uint16_t* bch = (uint16_t*)(inv + kPmRows);                   // [64][144] bf16
+  const int bidx = blockIdx.y, r0 = blockIdx.x * kPmRows;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, li = lane % 16, q = lane / 16;
+  const uint16_t* ab = a + (size_t)bidx * j * 128;
+  const uint16_t* bb = bmat + (size_t)bidx * kp * 128;
+
+  // Phase 1.  Rows past j repeat row j - 1 (padding rows of E), columns past kp are zero.
+  u32x4_t afr[4];
+  {
+    const u32x4_t* src = (const u32x4_t*)(ab + (size_t)min(r0 + li, j - 1) * 128) + 4 * q;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) afr[t] = src[t];
+  }
+  for (int ct = wave; ct < kpp / 16; ct += 4) {
+    const int col = ct * 16 + li;
+    u32x4_t bfr[4];
+    const u32x4_t* bsrc = (const u32x4_t*)(bb + (size_t)min(col, kp - 1) * 128) + 4 * q;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bfr[t] = bsrc[t];
+    f64x4_t acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int st = 0; st < 32; ++st) {
+      const int t = st / 8, w = (st % 8) / 2, hf = st % 2;
+      acc = mfma16x16x4_f64(bf16_half_f64(afr[t][w], hf), bf16_half_f64(bfr[t][w], hf), acc);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)  // D row 4 v + q, column li
+      praw[(4 * v + q) * ps + col] = col < kp ? f32_to_bf16((float)acc[v]) : (uint16_t)0;
+  }
+  __syncthreads();
+
+  // Phase 2: inv = 1 / sqrt(sum + 1e-8), 16 threads per row.
+  {
+    const int r = tid / 16, sub = tid % 16;
+    double sq = 0.0;
+    for (int k = sub; k < kp; k += 16) {
+      const double v = (double)bf16_to_f32(praw[r * ps + k]);
+      sq += v * v;
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+    if (sub == 0) inv[r] = 1.0 / sqrt(sq + 1e-8);
+  }
+  __syncthreads();
+  if (profile) {
+    const int nreal = max(0, min(kPmRows, j - r0));
+    float* pb = profile + (size_t)bidx * j * kp;
+    for (int t = tid; t < nreal * kp; t += 256) {
+      const int r = t / kp, k = t % kp;
+      pb[(size_t)(r0 + r) * kp + k] = (float)((double)bf16_to_f32(praw[r * ps + k]) * inv[r]);
+    }
+  }
+
+  // Phase 3.
+  f64x4_t e0 = {0.0, 0.0, 0.0, 0.0}, e1 = {0.0, 0.0, 0.0, 0.0};
+  const int dd0 = 32 * wave + li, dd1 = dd0 + 16;
+  for (int c = 0; c < kpp; c += kPmChunk) {
+    __syncthreads();  // the previous chunk is consumed
+    for (int t = tid; t < kPmChunk * 16; t += 256) {
+      const int row = t / 16, piece = t % 16;
+      *(u32x4_t*)(bch + row * kPmChunkStride + piece * 8) =
+          *((const u32x4_t*)(bb + (size_t)min(c + row, kp - 1) * 128) + piece);
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int st = 0; st < kPmChunk / 4; ++st) {
+      const int kl = 4 * st + q;
+      const double av = (double)bf16_to_f32(praw[li * ps + c + kl]);
+      e0 = mfma16x16x4_f64(av, (double)bf16_to_f32(bch[kl * kPmChunkStride + dd0]), e0);
+      e1 = mfma16x16x4_f64(av, (double)bf16_to_f32(bch[kl * kPmChunkStride + dd1]), e1);
+    }
+  }
+  uint16_t* hb = e_hi + (size_t)bidx * jpad * 128;
+  uint16_t* lb = e_lo + (size_t)bidx * jpad * 128;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int i = 4 * v + q, row = r0 + i;
+    if (row >= jpad) continue;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const double e = (hh ? e1[v] : e0[v]) * inv[i];
+      const uint16_t hi = f32_to_bf16((float)e);
+      const uint16_t lo = f32_to_bf16((float)(e - (double)bf16_to_f32(hi)));
+      const int dd = hh ? dd1 : dd0;
+      hb[(size_t)row * 128 + dd] = hi;
+      lb[(size_t)row * 128 + dd] = lo;
+    }
+  }
+}
+
 // --------------------------------------------------------------------------------------- assign
 // Block = 4 waves x 128 tokens (4 MFMA column blocks of 32 per wave); the token rows stay in
 // registers as the MFMA B operand for the whole pass.  E_hi and E_lo stream through LDS in chunks
@@ -273,7 +400,12 @@ static size_t prep_smem(int rows, int kp) {
 
 static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uint16_t* e_lo, float* profile, int bh,
                        int j, int kp, int jpad, hipStream_t stream) {
-  // Few rows (the query side) -> 2 rows per block for more blocks; many rows -> 8 rows per block.
+  if (kp <= kPmMaxKp) {
+    hipLaunchKernelGGL(cocluster_prep_mfma_kernel, dim3(jpad / kPmRows, bh), dim3(256), pm_smem(kp), stream, a, b,
+                       e_hi, e_lo, profile, j, kp, jpad);
+    return check_launch("svoo_cocluster_prep");
+  }
+  // Wide profiles: the vector kernel.  Few rows -> 2 rows per block for more blocks; many -> 8.
   if (j >= 512 && (size_t)8 * kp * sizeof(float) <= (size_t)kPrepMaxLds) {
     hipLaunchKernelGGL(cocluster_prep_kernel<8>, dim3(jpad / 8, bh), dim3(256), prep_smem(8, kp), stream, a, b, e_hi,
                        e_lo, profile, j, kp, jpad);

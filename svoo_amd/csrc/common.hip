@@ -75,11 +75,29 @@ __global__ void probe_kernel(float* out32, float* out16) {
   for (int r = 0; r < 4; ++r) out16[l * 4 + r] = c4[r];
 }
 
+// fp64 16x16x4 MFMA, index-coded as above: D[i][j] = 64 i + j when A[i][k] sits in lane i + 16 k,
+// B[k][j] in lane j + 16 k, and D[i][j] in lane j + 16 (i % 4), element i / 4.
+__global__ void probe_f64_kernel(double* out) {
+  const int l = threadIdx.x, i = l % 16, k = l / 16;
+  const double a1 = k == 0 ? (double)i : 0.0, b1 = k == 0 ? 64.0 : 0.0;
+  const double a2 = k == 0 ? 1.0 : 0.0, b2 = k == 0 ? (double)i : 0.0;
+  f64x4_t c = {0.0, 0.0, 0.0, 0.0};
+  c = mfma16x16x4_f64(a1, b1, c);
+  c = mfma16x16x4_f64(a2, b2, c);
+  for (int r = 0; r < 4; ++r) out[l * 4 + r] = c[r];
+}
+
 }  // namespace svoo
 
 extern "C" int svoo_version(void) { return 100; }
 
 extern "C" const char* svoo_last_error(void) { return svoo::g_last_error; }
+
+extern "C" int svoo_probe_mfma_f64_layout(double* out, void* stream) {
+  SVOO_REQUIRE(out, SVOO_ERR_INVALID_ARG, "svoo_probe_mfma_f64_layout: null output");
+  hipLaunchKernelGGL(svoo::probe_f64_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, out);
+  return svoo::check_launch("svoo_probe_mfma_f64_layout");
+}
 
 extern "C" int svoo_probe_mfma_layout(float* out32, float* out16, void* stream) {
   SVOO_REQUIRE(out32 && out16, SVOO_ERR_INVALID_ARG, "svoo_probe_mfma_layout: null output");

@@ -44,6 +44,13 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t 
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// 16x16x4 fp64 MFMA.  A[i][k]: lane i + 16 k; B[k][j]: lane j + 16 k; D[i][j]: lane j + 16 (i % 4),
+// element i / 4 (measured by svoo_probe_mfma_f64_layout).
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f64x4_t mfma16x16x4_f64(double a, double b, f64x4_t c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }

@@ -50,6 +50,18 @@ def test_mfma_operand_layout(gpu):
             assert c16[l, r] == 16 * m + n, (l, r, c16[l, r])
 
 
+def test_mfma_f64_operand_layout(gpu):
+    from svoo_amd import _lib
+
+    say("mfma f64 layout probe")
+    o = torch.zeros(64 * 4, dtype=torch.float64, device=gpu)
+    _lib.call("svoo_probe_mfma_f64_layout", o.data_ptr(), _lib.stream_of(gpu))
+    torch.cuda.synchronize()
+    c = o.cpu().numpy().reshape(64, 4)
+    want = np.array([[64 * (4 * r + l // 16) + l % 16 for r in range(4)] for l in range(64)], np.float64)
+    assert np.array_equal(c, want), c.tolist()
+
+
 @pytest.mark.parametrize("bh,n,k", [(3, 5000, 37), (2, 1024, 1), (1, 1, 1), (2, 777, 2000), (4, 2049, 1000)])
 def test_cluster_sort_bit_exact(gpu, bh, n, k):
     from svoo_amd.permute import cluster_sort
