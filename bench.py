@@ -19,6 +19,7 @@ the same inputs, rank 0 only).
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import os
 import sys
@@ -355,11 +356,13 @@ def main_dit(args):
                 for ly in range(layers):
                     for hd in range(heads):
                         f.write(f"{st + 1},{ly},{hd},{rho[st, ly, hd]:.4f}\n")
-        procs = replace_wan_attention(
-            pipe, height, width, frames, first_layers_fp=0, first_times_fp=1000.0, num_q_centroids=256,
-            num_k_centroids=1024, top_p_kmeans=top_p, min_kc_ratio=0.10, kmeans_iter_init=2, kmeans_iter_step=2,
-            start_reuse_step=None, reuse_interval=1, use_dynamic_min_kc_ratio=True, sparsity_csv_path=str(csv),
-            dynamic_min_kc_ratio_min=dmin, dynamic_min_kc_ratio_max=dmax, processor_cls=Proc)
+        # the profile loader reports on stdout; keep stdout for the one JSON line
+        with contextlib.redirect_stdout(sys.stderr):
+            procs = replace_wan_attention(
+                pipe, height, width, frames, first_layers_fp=0, first_times_fp=1000.0, num_q_centroids=256,
+                num_k_centroids=1024, top_p_kmeans=top_p, min_kc_ratio=0.10, kmeans_iter_init=2, kmeans_iter_step=2,
+                start_reuse_step=None, reuse_interval=1, use_dynamic_min_kc_ratio=True, sparsity_csv_path=str(csv),
+                dynamic_min_kc_ratio_min=dmin, dynamic_min_kc_ratio_max=dmax, processor_cls=Proc)
     n = Proc.num_frame * Proc.frame_size
     assert n == 32760, n
     timesteps = iter(np.linspace(999.0, 600.0, 10 * nsteps))
