@@ -148,6 +148,16 @@ int svoo_vbsa_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const
                   void* workspace, size_t ws_bytes, int32_t* status, void* stream);
 int svoo_vbsa_segments(const uint8_t* map, const int32_t* k_sizes, int bh, int qn, int kn, int32_t* seg_start,
                        int32_t* seg_len, int32_t* seg_count, void* stream);
+/* svoo_vbsa_fused_fwd: the same attention on Q, K, V in token order ([BH][S][D], BH = B*H), read through the
+ *   clusters' stable sort (q_sorted_idx / k_sorted_idx [BH][S], as svoo_co_cluster returns them), with each
+ *   output row written to its token's place in o_bshd [B][S][H][D].  Equal to svoo_permute_rows (Q),
+ *   svoo_permute_rows2 (K, V), svoo_vbsa_fwd and svoo_unpermute_rows_bshd in sequence, in one pass.
+ *   Replaces the permutes, dynamic_block_sparse_fwd_flashinfer and apply_inverse_permutation_triton +
+ *   transpose of svoo/models/wan/attention.py:1037-1042, 1196-1215. */
+int svoo_vbsa_fused_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* q_sorted_idx,
+                        const int32_t* k_sorted_idx, const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes,
+                        uint16_t* o_bshd, int bh, int heads, int s, int d, int qn, int kn, void* workspace,
+                        size_t ws_bytes, int32_t* status, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * EAR (error-aware routing with centroid compensation).  All token inputs are cluster-contiguous

@@ -27,6 +27,7 @@ __all__ = [
     "identify_dynamic_map",
     "block_mask_lengths",
     "dynamic_block_sparse_fwd",
+    "dynamic_block_sparse_fwd_fused",
     "dynamic_block_sparse_fwd_flashinfer",
     "dynamic_block_sparse_fwd_triton",
     "vbsa_segments",
@@ -377,6 +378,43 @@ def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate
     if validate and int(status.item()) != 0:
         raise AssertionError("cluster sizes of every head must sum to S (qc_size / kc_size)")
     return out.reshape(b, h, s, d)
+
+
+def dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, qc_size, kc_size, q_sorted_idx, k_sorted_idx,
+                                   *, validate: bool = True):
+    """Permute, variable-block-sparse attention and inverse permutation in one kernel.
+
+    ``query, key, value [B, H, S, D]`` in token order; ``q_sorted_idx`` / ``k_sorted_idx [B*H, S]`` are the stable
+    cluster sorts (``co_cluster_tokens_full``'s ``q_sorted_idx`` / ``k_sorted_idx``).  Returns ``[B, S, H*D]``,
+    equal to :func:`dynamic_block_sparse_fwd` on the permuted tensors followed by the inverse permutation and
+    ``transpose(1, 2).flatten(2, 3)`` (``svoo/models/wan/attention.py:1037-1042, 1196-1215``).
+    """
+    assert query.is_cuda and key.is_cuda and value.is_cuda, "Inputs must be CUDA tensors"
+    if query.dtype != torch.bfloat16 or key.dtype != query.dtype or value.dtype != query.dtype:
+        raise TypeError("dynamic_block_sparse_fwd_fused: the MI355X path computes in bfloat16")
+    b, h, s, d = query.shape
+    assert key.shape == query.shape and value.shape == query.shape, "q, k, v must share one shape"
+    qn = qc_size.shape[-1]
+    kn = kc_size.shape[-1]
+    assert dynamic_map.shape == (b, h, qn, kn), "dynamic_map must be [B, H, Qc, Kc]"
+    dev = query.device
+    bh = b * h
+    qq, kk, vv = (t.reshape(bh, s, d).contiguous() for t in (query, key, value))
+    qi = q_sorted_idx.to(device=dev, dtype=torch.int32).reshape(bh, s).contiguous()
+    ki = k_sorted_idx.to(device=dev, dtype=torch.int32).reshape(bh, s).contiguous()
+    m = dynamic_map.to(device=dev, dtype=torch.bool).reshape(bh, qn, kn).contiguous()
+    qs = qc_size.to(device=dev, dtype=torch.int32).reshape(bh, qn).contiguous()
+    ks = kc_size.to(device=dev, dtype=torch.int32).reshape(bh, kn).contiguous()
+    out = torch.empty(b, s, h * d, dtype=query.dtype, device=dev)
+    L = _lib.lib()
+    ws = _lib.workspace(L.svoo_vbsa_workspace_size(bh, s, qn, kn), dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev) if validate else None
+    _lib.call("svoo_vbsa_fused_fwd", qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), qi.data_ptr(), ki.data_ptr(),
+              m.data_ptr(), qs.data_ptr(), ks.data_ptr(), out.data_ptr(), bh, h, s, d, qn, kn, ws.data_ptr(),
+              ws.numel(), _lib.ptr(status), _lib.stream_of(dev))
+    if validate and int(status.item()) != 0:
+        raise AssertionError("cluster sizes of every head must sum to S (qc_size / kc_size)")
+    return out
 
 
 def dynamic_block_sparse_fwd_flashinfer(q, k, v, block_mask_map, block_row_sz, block_col_sz, is_cpu: bool = True):

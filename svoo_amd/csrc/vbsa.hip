@@ -18,6 +18,10 @@
 //     units are busy at the same time;
 //   * fp32 online softmax (exp2 with the scale folded in), P rounded to bf16 for the PV MFMA, as
 //     the reference's Triton kernel does; rows of a cluster with no active keys are written as 0.
+// Fused variant (IDX): Q, K and V stay in token order; the kernel reads them through the clusters'
+// sorted indices (query rows when loaded, key rows when the row tables are resolved) and writes each
+// output row to its token's place in [B, S, H, D], so the permutes and the inverse permutation around
+// the attention are not separate passes.
 // EAR variant (centroid compensation): the KV stream continues after the active tokens with the
 // (key, value) centroids of the inactive clusters, each scored q . kc_j / sqrt(D) + log(|K_j| + 1e-6),
 // so one online softmax covers both (the reference's token attention + log-sum-exp merge).
@@ -217,13 +221,14 @@ __device__ __forceinline__ int cursor_row(KvCursor& c, const int32_t* seg_start,
 // K(t+1) Q^T} and a VALU phase V(t) = {softmax of S(t) -> P(t)}; group B runs one half-step behind
 // group A, so in every half-step one wave per SIMD does MFMA work while the other does VALU work.
 // Group B also issues the LDS DMA of the next K/V tiles and resolves their token rows.
-template <int QB, bool EAR>
+template <int QB, bool EAR, bool IDX>
 __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) vbsa_attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const uint8_t* __restrict__ map, const int32_t* __restrict__ ks, uint16_t* __restrict__ o, int s, int qn, int kn,
     int cap, long long total_items, const int32_t* __restrict__ qoff, const int32_t* __restrict__ koff,
-    const int32_t* __restrict__ items, const int32_t* __restrict__ nitems, float scale_log2) {
+    const int32_t* __restrict__ items, const int32_t* __restrict__ nitems, float scale_log2,
+    const int32_t* __restrict__ q_idx, const int32_t* __restrict__ k_idx, int heads) {
   constexpr int kQTile = VbsaCfg<QB>::kQTile;
   constexpr int kThreads = kVWaves * kWave;
   constexpr int kDmaIt = kKT / (4 * 4);  // 4-row DMA groups per group-B wave per tile and matrix
@@ -252,6 +257,15 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   const uint16_t* kb = k + head;
   const uint16_t* vb = v + head;
   uint16_t* ob = o + head;
+  // IDX: sorted position -> token row of this head, and the output row of a sorted query position
+  const int32_t* qix = IDX ? q_idx + (size_t)b * s : nullptr;
+  const int32_t* kix = IDX ? k_idx + (size_t)b * s : nullptr;
+  auto out_row = [&](int r) -> uint16_t* {
+    if constexpr (IDX)
+      return o + (((size_t)(b / heads) * s + qix[r]) * heads + (b % heads)) * 128;
+    else
+      return ob + (size_t)r * 128;
+  };
   // EAR: the centroid rows are addressed from the token base of the head, as rows at a signed offset
   // (the host checks that the buffers are 256-byte congruent and that every row index fits int32), so
   // the DMA path is the same as for token rows.
@@ -282,7 +296,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     // Empty row: zero output (reference semantics, svoo/co_clustering.py:1102-1104).
     for (int idx = tid; idx < (q1 - q0) * 16; idx += kThreads) {
       const int r = idx / 16, c = idx % 16;
-      ((u32x4_t*)(ob + (size_t)(q0 + r) * 128))[c] = u32x4_t{0u, 0u, 0u, 0u};
+      ((u32x4_t*)out_row(q0 + r))[c] = u32x4_t{0u, 0u, 0u, 0u};
     }
     return;
   }
@@ -292,7 +306,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   u32x4_t qop[8];
   {
     const int row = min(qrow0 + l32, q1 - 1);
-    const u32x4_t* src = (const u32x4_t*)(qb + (size_t)row * 128);
+    const u32x4_t* src = (const u32x4_t*)(qb + (size_t)(IDX ? qix[row] : row) * 128);
 #pragma unroll
     for (int ks2 = 0; ks2 < 8; ++ks2) qop[ks2] = src[ks2 * 2 + h];
   }
@@ -304,14 +318,17 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   // Row tables: wave 4 resolves K tiles, wave 5 V tiles (lane = tile position).
   // Rows past the stream repeat its last token row (0 when an EAR row has no active tokens); EAR
   // centroid j of the K (V) table is row crow_k + j (crow_v + j).
-  const int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
+  int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
+  if constexpr (IDX) last_row = kix[last_row];
   KvCursor cursor;
   if ((wave == 4 || wave == 5) && nseg > 0) cursor_init(cursor, seg_start, seg_cum, nseg, min(lane, total_tok - 1));
   const int crow = wave == 4 ? crow_k : crow_v;  // the resolving waves: 4 for K, 5 for V
   auto resolve = [&](int32_t* tab, int t) {
     const int p = t * kKT + lane;
-    if (p < total_tok)
-      tab[lane] = cursor_row(cursor, seg_start, seg_cum, p);
+    if (p < total_tok) {
+      const int pos = cursor_row(cursor, seg_start, seg_cum, p);
+      tab[lane] = IDX ? kix[pos] : pos;
+    }
     else if (EAR && p < total)
       tab[lane] = crow + cent_idx[p - total_tok];
     else
@@ -558,7 +575,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   const int row = qrow0 + l32;
   if (row < q1) {
-    uint16_t* dst = ob + (size_t)row * 128;
+    uint16_t* dst = out_row(row);
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -634,11 +651,11 @@ extern "C" size_t svoo_vbsa_workspace_size(int bh, int s, int qn, int kn) {
 }
 
 namespace {
-template <bool EAR>
+template <bool EAR, bool IDX = false>
 int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* kc,
                 const uint16_t* vc, const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes, uint16_t* o,
                 int bh, int s, int d, int qn, int kn, void* workspace, size_t ws_bytes, int32_t* status,
-                void* stream) {
+                void* stream, const int32_t* q_idx = nullptr, const int32_t* k_idx = nullptr, int heads = 1) {
   SVOO_REQUIRE(q && k && v && map && q_sizes && k_sizes && o && (!EAR || (kc && vc)), SVOO_ERR_INVALID_ARG,
                "%s: null pointer", name);
   SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "%s: D=%d (only 128 supported)", name, d);
@@ -675,9 +692,9 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   SVOO_REQUIRE(nblocks < (1ll << 31), SVOO_ERR_UNSUPPORTED, "%s: too many work items", name);
   const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)d));
   const size_t smem = (size_t)((EAR ? 4 : 2) * kn + 1) * sizeof(int32_t);
-  hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR>), dim3((unsigned)nblocks), dim3(kVWaves * kWave), smem, st, q,
-                     k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items, nitems,
-                     scale_log2);
+  hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX>), dim3((unsigned)nblocks), dim3(kVWaves * kWave), smem,
+                     st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items, nitems,
+                     scale_log2, q_idx, k_idx, heads);
   return check_launch(name);
 }
 }  // namespace
@@ -687,6 +704,17 @@ extern "C" int svoo_vbsa_fwd(const uint16_t* q, const uint16_t* k, const uint16_
                              int kn, void* workspace, size_t ws_bytes, int32_t* status, void* stream) {
   return vbsa_launch<false>("svoo_vbsa_fwd", q, k, v, nullptr, nullptr, map, q_sizes, k_sizes, o, bh, s, d, qn, kn,
                             workspace, ws_bytes, status, stream);
+}
+
+extern "C" int svoo_vbsa_fused_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* q_sorted_idx,
+                                   const int32_t* k_sorted_idx, const uint8_t* map, const int32_t* q_sizes,
+                                   const int32_t* k_sizes, uint16_t* o_bshd, int bh, int heads, int s, int d, int qn,
+                                   int kn, void* workspace, size_t ws_bytes, int32_t* status, void* stream) {
+  SVOO_REQUIRE(q_sorted_idx && k_sorted_idx, SVOO_ERR_INVALID_ARG, "svoo_vbsa_fused_fwd: null index");
+  SVOO_REQUIRE(heads > 0 && bh % heads == 0, SVOO_ERR_INVALID_ARG, "svoo_vbsa_fused_fwd: bh=%d not a multiple of H=%d",
+               bh, heads);
+  return vbsa_launch<false, true>("svoo_vbsa_fused_fwd", q, k, v, nullptr, nullptr, map, q_sizes, k_sizes, o_bshd, bh,
+                                  s, d, qn, kn, workspace, ws_bytes, status, stream, q_sorted_idx, k_sorted_idx, heads);
 }
 
 extern "C" int svoo_vbsa_ear_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* k_cent,

@@ -27,7 +27,8 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
-from .co_clustering import block_mask_lengths, co_cluster_tokens_full, dynamic_block_sparse_fwd
+from .co_clustering import (block_mask_lengths, co_cluster_tokens_full, dynamic_block_sparse_fwd,
+                            dynamic_block_sparse_fwd_fused)
 from .ear import dynamic_block_sparse_prune_fwd, ear_map_and_value_centroids
 from .sparsity.exact import compute_exact_attention_sparsity, format_sparsity_log, has_completed_sparsity_entry
 from .permute import apply_inverse_permutation, apply_inverse_permutation_bshd, permute_pair_by_indices
@@ -95,6 +96,11 @@ class WanAttn_SAPAttn_Processor:
     use_svoo = True
     use_ear = False
     ear_gamma = 1.0
+    # Run the SAP attention on token-order Q/K/V through the sorted indices (one kernel instead of
+    # permute + attention + inverse permutation; the same bits, and no permuted copies of Q/K/V/O).
+    # Off by default: the gathered K/V rows cost more in the attention kernel than the separate
+    # permute passes (36.7 vs 36.2 ms at the Wan-14B 720p shape).
+    fuse_permutes = False
     use_global_constraints = False
     use_routing_transformer_strategy = False
     enable_mem_save = bool(int(os.environ.get("SVOO_ENABLE_MEM_SAVE", "1")))
@@ -347,6 +353,10 @@ class WanAttn_SAPAttn_Processor:
                                    min_kc_ratio=min_kc_ratio, q_sizes=q_sizes, k_sizes=k_sizes, v_centroids=v_cent,
                                    **parts)
             return q_perm, k_perm, v_perm, dynamic_map, q_sizes, k_sizes, r["q_sorted_idx"], kcv, v_cent
+        dynamic_map = self._block_mask(r, cfg, num_heads, dim, q_sizes, k_sizes, min_kc_ratio)
+        return q_perm, k_perm, v_perm, dynamic_map, q_sizes, k_sizes, r["q_sorted_idx"]
+
+    def _block_mask(self, r, cfg, num_heads, dim, q_sizes, k_sizes, min_kc_ratio):
         dynamic_map, lengths = block_mask_lengths(
             r["qcentroids"].view(cfg, num_heads, self.num_q_centroids, dim),
             r["kcentroids"].view(cfg, num_heads, self.num_k_centroids, dim),
@@ -354,7 +364,24 @@ class WanAttn_SAPAttn_Processor:
         )
         self._last_call = dict(clustering=r, map=dynamic_map, lengths=lengths, min_kc_ratio=min_kc_ratio,
                                q_sizes=q_sizes, k_sizes=k_sizes)
-        return q_perm, k_perm, v_perm, dynamic_map, q_sizes, k_sizes, r["q_sorted_idx"]
+        return dynamic_map
+
+    def fused_sparse_attention(self, query, key, value):
+        """The SAP path of :meth:`attention_core_logic` without separate permute passes: cluster, block mask,
+        then one kernel that reads Q/K/V through the sorted indices and writes ``[1, S, H*D]`` in token order
+        (the same values as permute + ``dynamic_block_sparse_fwd`` + inverse permutation)."""
+        cfg, num_heads, seq_len, dim = query.size()
+        r = self.kmeans_clustering(query, key, self.layer_idx)
+        self._mark("cluster")
+        min_kc_ratio = self._get_min_kc_ratio_for_heads_from_step(self.current_inference_step, num_heads)
+        q_sizes = r["qsizes"].view(cfg, num_heads, self.num_q_centroids)
+        k_sizes = r["ksizes"].view(cfg, num_heads, self.num_k_centroids)
+        dynamic_map = self._block_mask(r, cfg, num_heads, dim, q_sizes, k_sizes, min_kc_ratio)
+        self._mark("mask")
+        out = dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, q_sizes, k_sizes, r["q_sorted_idx"],
+                                             r["k_sorted_idx"], validate=False)
+        self._mark("attention")
+        return out
 
     def attention_core_logic(self, query, key, value, timestep):
         """SVOO attention for ``[1, H, S, D]`` Q/K/V; returns ``[1, S, H*D]`` (``:1110-1216``)."""
@@ -387,6 +414,8 @@ class WanAttn_SAPAttn_Processor:
             return out.transpose(1, 2).flatten(2, 3)
 
         self._mark("start")
+        if not self.use_ear and self.fuse_permutes:
+            return self.fused_sparse_attention(query, key, value)
         perm = self.semantic_aware_permutation(query, key, value, timestep)
         q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, q_sorted_indices = perm[:7]
         self._mark("mask")

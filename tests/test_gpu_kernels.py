@@ -317,3 +317,36 @@ def test_golden_small_end_to_end(gpu):
     m0 = torch.from_numpy(g["map0"]).to(gpu)[None]
     out = dynamic_block_sparse_fwd(qp[None], kp, vp, m0, r["qsizes"][None], r["ksizes"][None])
     _attn_check(out[0], g["out_perm"].astype(np.float64))
+
+
+@pytest.mark.parametrize("h,qn,kn,s,density,seed", [(2, 12, 40, 3000, 0.3, 1), (3, 30, 200, 4096, 0.1, 3),
+                                                    (2, 4, 4, 333, 1.0, 4)])
+def test_fused_attention_equals_separate_passes(gpu, h, qn, kn, s, density, seed):
+    """Permute + attention + inverse permutation in one kernel gives the same bits as the three passes."""
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd, dynamic_block_sparse_fwd_fused
+    from svoo_amd.permute import apply_inverse_permutation_bshd, permute_pair_by_indices
+    from svoo_amd.processor import _permute_rows
+
+    say("fused vbsa", h, qn, kn, s, density)
+    r = np.random.default_rng(seed)
+
+    def sizes(c):
+        cuts = np.sort(r.integers(0, s + 1, size=(h, c - 1)), axis=1)
+        z = np.concatenate([np.zeros((h, 1), int), cuts, np.full((h, 1), s)], axis=1)
+        return np.diff(z, axis=1).astype(np.int32)[None]
+
+    qs, ks = sizes(qn), sizes(kn)
+    m = torch.from_numpy(r.random((1, h, qn, kn)) < density).to(gpu)
+    m[0, 0, 0, :] = False  # an empty row
+    qi = torch.from_numpy(np.stack([r.permutation(s) for _ in range(h)]).astype(np.int32)).to(gpu)
+    ki = torch.from_numpy(np.stack([r.permutation(s) for _ in range(h)]).astype(np.int32)).to(gpu)
+    _, q = rand_bf16((1, h, s, 128), seed, gpu)
+    _, k = rand_bf16((1, h, s, 128), seed + 1, gpu)
+    _, v = rand_bf16((1, h, s, 128), seed + 2, gpu)
+    qst, kst = torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu)
+    out = dynamic_block_sparse_fwd_fused(q, k, v, m, qst, kst, qi, ki)
+    qp = _permute_rows(q, qi)
+    kp, vp = permute_pair_by_indices(k, v, ki)
+    ref = apply_inverse_permutation_bshd(dynamic_block_sparse_fwd(qp, kp, vp, m, qst, kst), qi)
+    assert out.shape == (1, s, h * 128)
+    assert torch.equal(out, ref)

@@ -203,3 +203,31 @@ def test_hunyuan_double_stream_call_dense_gate(gpu):
     assert out_h.shape == (1, vl, dim) and out_e.shape == (1, ctx, dim)
     check(out_h, ref_h.cpu().numpy(), scale=float(ref_h.abs().max()))
     check(out_e, ref_e.cpu().numpy(), scale=float(ref_e.abs().max()))
+
+
+def test_wan_processor_fused_path_equals_separate_passes(gpu):
+    """``fuse_permutes`` runs the same attention in one kernel: identical output bits."""
+    from svoo_amd import synth
+    from svoo_amd.processor import WanAttn_SAPAttn_Processor
+
+    say("wan attention_core_logic fused vs separate permutes")
+    cfg = synth.SynthConfig("fuse-small", 61, 2, 3, 16, 20, 128, 24, 12, 32, 3, 0.1, 0.4, True, "bf16")
+    q, k, v = (x.to(gpu) for x in synth.make_qkv(cfg))
+    r = np.random.default_rng(6)
+    qi = torch.from_numpy(r.integers(0, cfg.video_tokens, size=(cfg.heads, 12))).to(gpu)
+    ki = torch.from_numpy(r.integers(0, cfg.video_tokens, size=(cfg.heads, 32))).to(gpu)
+    outs = []
+    for fused in (False, True):
+        class P(WanAttn_SAPAttn_Processor):
+            pass
+
+        P.num_frame, P.frame_size, P.context_length = cfg.frames, cfg.frame_size, 0
+        P.num_q_centroids, P.num_k_centroids = 12, 32
+        P.top_p_kmeans, P.min_kc_ratio = 0.7, 0.1
+        P.kmeans_iter_init = P.kmeans_iter_step = 3
+        P.first_times_fp, P.first_layers_fp = 1e9, 0
+        P.kmeans_init_idx = (qi, ki)
+        P.fuse_permutes = fused
+        outs.append(P(layer_idx=0).attention_core_logic(q, k, v, torch.tensor([100.0], device=gpu)))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
