@@ -42,7 +42,8 @@ struct VbsaCfg {
 // ------------------------------------------------------------------------------------------ plan
 __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* __restrict__ qs,
                                                                  const int32_t* __restrict__ ks, int s, int qn, int kn,
-                                                                 int qtile, int cap, int32_t* __restrict__ qoff,
+                                                                 int qtile, int cap, int half_ok,
+                                                                 int32_t* __restrict__ qoff,
                                                                  int32_t* __restrict__ koff,
                                                                  int32_t* __restrict__ items,
                                                                  int32_t* __restrict__ nitems,
@@ -97,8 +98,12 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
       qo[i] = (int32_t)(run & 0xffffffffll);
       const int t0 = (int)(run >> 32);
       const int nt = v > 0 ? (v + qtile - 1) / qtile : 0;
+      // a last tile of at most qtile / 2 queries is a half item (flag 0x8000) when the kernel has
+      // the LDS for a second KV stream
+      const int rem = v - (nt - 1) * qtile;
+      const int hflag = (half_ok && 2 * rem <= qtile) ? 0x8000 : 0;
       if (ok)
-        for (int t = 0; t < nt; ++t) items[(size_t)b * cap + t0 + t] = (i << 16) | t;
+        for (int t = 0; t < nt; ++t) items[(size_t)b * cap + t0 + t] = (i << 16) | t | (t == nt - 1 ? hflag : 0);
       run += ((long long)nt << 32) | (long long)(uint32_t)v;
     }
     if (tid == 0) {
@@ -221,7 +226,12 @@ __device__ __forceinline__ int cursor_row(KvCursor& c, const int32_t* seg_start,
 // K(t+1) Q^T} and a VALU phase V(t) = {softmax of S(t) -> P(t)}; group B runs one half-step behind
 // group A, so in every half-step one wave per SIMD does MFMA work while the other does VALU work.
 // Group B also issues the LDS DMA of the next K/V tiles and resolves their token rows.
-template <int QB, bool EAR, bool IDX>
+// Half items (HC kernels only: a second set of K/V buffers in LDS): a last tile of at most 128
+// queries is taken by both groups, each wave of a group holding the same 32 queries as its partner
+// in the other group; group A walks the even tiles of the KV stream (stream 0), group B the odd
+// ones (stream 1), on the same half-step schedule, and the two online-softmax states are merged
+// through LDS at the end, so such an item costs about half the time of a full one.
+template <int QB, bool EAR, bool IDX, bool HC>
 __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) vbsa_attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
@@ -234,8 +244,11 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   constexpr int kDmaIt = kKT / (4 * 4);  // 4-row DMA groups per group-B wave per tile and matrix
   __shared__ __attribute__((aligned(16))) uint16_t k_s0[kKT * 128], k_s1[kKT * 128];
   __shared__ __attribute__((aligned(16))) uint16_t v_s0[kKT * 128], v_s1[kKT * 128];
+  // stream 1 of a half item
+  constexpr int kS1 = HC ? kKT * 128 : 8;
+  __shared__ __attribute__((aligned(16))) uint16_t k1_s0[kS1], k1_s1[kS1], v1_s0[kS1], v1_s1[kS1];
   __shared__ long long red[kVWaves];
-  __shared__ int32_t rowtab[2][2][kKT];  // [K/V][slot][tile position] -> token row
+  __shared__ int32_t rowtab[HC ? 2 : 1][2][2][kKT];  // [stream][K/V][slot][tile position] -> token row
   extern __shared__ int32_t seg_mem[];  // seg_start[kn], seg_cum[kn + 1] (EAR: cent_idx[kn], cent_bias[kn])
 
   const long long item = xcd_item(blockIdx.x);
@@ -243,7 +256,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   const int b = (int)(item / cap), local = (int)(item % cap);
   if (local >= nitems[b]) return;
   const int packed = items[(size_t)b * cap + local];
-  const int ci = packed >> 16, tile = packed & 0xffff;
+  const int ci = packed >> 16, tile = packed & 0x7fff;
+  const bool half = HC && (packed & 0x8000) != 0;
   const int32_t* qo = qoff + (size_t)b * (qn + 1);
   const int q0 = qo[ci] + tile * kQTile;
   const int q1 = min(qo[ci + 1], q0 + kQTile);
@@ -300,7 +314,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     }
     return;
   }
-  const int qrow0 = q0 + (group_b ? 128 : 0) + wg * 32;
+  // full item: group A owns queries 0-127, group B 128-255; half item: both own queries 0-127
+  const int qrow0 = q0 + ((group_b && !half) ? 128 : 0) + wg * 32;
   const bool active = qrow0 < q1;
 
   u32x4_t qop[8];
@@ -315,14 +330,16 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   for (int db = 0; db < 4; ++db) acc[db] = f32x16_t{};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  // Row tables: wave 4 resolves K tiles, wave 5 V tiles (lane = tile position).
+  // Row tables: wave 4 resolves K tiles, wave 5 V tiles (lane = tile position); in a half item waves 4
+  // and 5 resolve stream 0 (even tiles), waves 6 and 7 stream 1 (odd tiles).
   // Rows past the stream repeat its last token row (0 when an EAR row has no active tokens); EAR
   // centroid j of the K (V) table is row crow_k + j (crow_v + j).
   int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
   if constexpr (IDX) last_row = kix[last_row];
   KvCursor cursor;
-  if ((wave == 4 || wave == 5) && nseg > 0) cursor_init(cursor, seg_start, seg_cum, nseg, min(lane, total_tok - 1));
-  const int crow = wave == 4 ? crow_k : crow_v;  // the resolving waves: 4 for K, 5 for V
+  if ((wave == 4 || wave == 5 || (half && wave >= 6)) && nseg > 0)
+    cursor_init(cursor, seg_start, seg_cum, nseg, min((wave >= 6 ? kKT : 0) + lane, total_tok - 1));
+  const int crow = (wave & 1) ? crow_v : crow_k;  // the resolving waves: even for K, odd for V
   auto resolve = [&](int32_t* tab, int t) {
     const int p = t * kKT + lane;
     if (p < total_tok) {
@@ -504,69 +521,191 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   };
   // Group B housekeeping at the start of its V(t): DMA K(t+2), V(t+1); resolve K(t+3), V(t+2).
   auto fetch = [&](int t, uint16_t* kdst, uint16_t* vdst) {
-    if (t + 2 < ntiles) dma(kb, rowtab[0][t & 1], kdst);
-    if (t + 1 < ntiles) dma(vb, rowtab[1][(t + 1) & 1], vdst);
-    if (wave == 4 && t + 3 < ntiles) resolve(rowtab[0][(t + 1) & 1], t + 3);
-    if (wave == 5 && t + 2 < ntiles) resolve(rowtab[1][t & 1], t + 2);
+    if (t + 2 < ntiles) dma(kb, rowtab[0][0][t & 1], kdst);
+    if (t + 1 < ntiles) dma(vb, rowtab[0][1][(t + 1) & 1], vdst);
+    if (wave == 4 && t + 3 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 3);
+    if (wave == 5 && t + 2 < ntiles) resolve(rowtab[0][1][t & 1], t + 2);
   };
 
-  // Prologue: tables K(0), K(1), V(0), V(1); DMA K(0), V(0) -> buffers 0, K(1) -> K buffer 1;
-  // S(0) everywhere, V(0) in group A; table K(2).
-  if (wave == 4) {
-    resolve(rowtab[0][0], 0);
-    if (ntiles > 1) resolve(rowtab[0][1], 1);
-  }
-  if (wave == 5) {
-    resolve(rowtab[1][0], 0);
-    if (ntiles > 1) resolve(rowtab[1][1], 1);
-  }
-  __syncthreads();
-  if (group_b) {
-    dma(kb, rowtab[0][0], k_s0);
-    dma(vb, rowtab[1][0], v_s0);
-    if (ntiles > 1) dma(kb, rowtab[0][1], k_s1);
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
-  __syncthreads();
-  if (active) scores(k_s0);
-  if (active && !group_b) vphase(0);
-  if (wave == 4 && ntiles > 2) resolve(rowtab[0][0], 2);
-  __syncthreads();
+  if (!half) {
+    // Prologue: tables K(0), K(1), V(0), V(1); DMA K(0), V(0) -> buffers 0, K(1) -> K buffer 1;
+    // S(0) everywhere, V(0) in group A; table K(2).
+    if (wave == 4) {
+      resolve(rowtab[0][0][0], 0);
+      if (ntiles > 1) resolve(rowtab[0][0][1], 1);
+    }
+    if (wave == 5) {
+      resolve(rowtab[0][1][0], 0);
+      if (ntiles > 1) resolve(rowtab[0][1][1], 1);
+    }
+    __syncthreads();
+    if (group_b) {
+      dma(kb, rowtab[0][0][0], k_s0);
+      dma(vb, rowtab[0][1][0], v_s0);
+      if (ntiles > 1) dma(kb, rowtab[0][0][1], k_s1);
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    if (active) scores(k_s0);
+    if (active && !group_b) vphase(0);
+    if (wave == 4 && ntiles > 2) resolve(rowtab[0][0][0], 2);
+    __syncthreads();
 
-  // Half-steps h = 0 .. 2T-1 (unrolled by 4: tile parity fixes the buffers).
-  //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1)        B: h = 2t -> V(t) + fetch;  h = 2t+1 -> M(t)
-  for (int t = 0; t < ntiles; t += 2) {
-    // tile t (even): V(t) in v_s0, K(t+1) in k_s1
-    if (!group_b) {
-      if (active) mphase(t, v_s0, k_s1);
-    } else {
-      fetch(t, k_s0, v_s1);
-      if (active) vphase(t);
+    // Half-steps h = 0 .. 2T-1 (unrolled by 4: tile parity fixes the buffers).
+    //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1)        B: h = 2t -> V(t) + fetch;  h = 2t+1 -> M(t)
+    for (int t = 0; t < ntiles; t += 2) {
+      // tile t (even): V(t) in v_s0, K(t+1) in k_s1
+      if (!group_b) {
+        if (active) mphase(t, v_s0, k_s1);
+      } else {
+        fetch(t, k_s0, v_s1);
+        if (active) vphase(t);
+      }
+      __syncthreads();
+      if (!group_b) {
+        if (active && t + 1 < ntiles) vphase(t + 1);
+      } else {
+        if (active) mphase(t, v_s0, k_s1);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __syncthreads();
+      if (t + 1 >= ntiles) break;
+      // tile t+1 (odd): V(t+1) in v_s1, K(t+2) in k_s0
+      if (!group_b) {
+        if (active) mphase(t + 1, v_s1, k_s0);
+      } else {
+        fetch(t + 1, k_s1, v_s0);
+        if (active) vphase(t + 1);
+      }
+      __syncthreads();
+      if (!group_b) {
+        if (active && t + 2 < ntiles) vphase(t + 2);
+      } else {
+        if (active) mphase(t + 1, v_s1, k_s0);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __syncthreads();
+    }
+  } else if constexpr (HC) {
+    // Half item: local tile u of stream x is global tile 2u + x; stream 0 (n0 tiles) lives in the
+    // k_s / v_s buffers and is used by group A, stream 1 (n1 tiles) in k1_s / v1_s, used by group B.
+    // Group B fetches both streams with the full item's timing; waves 4-7 resolve the four tables.
+    const int n0 = (ntiles + 1) / 2, n1 = ntiles / 2;
+    auto fetch2 = [&](int u, uint16_t* kdst0, uint16_t* vdst0, uint16_t* kdst1, uint16_t* vdst1) {
+      if (u + 2 < n0) dma(kb, rowtab[0][0][u & 1], kdst0);
+      if (u + 1 < n0) dma(vb, rowtab[0][1][(u + 1) & 1], vdst0);
+      if (u + 2 < n1) dma(kb, rowtab[1][0][u & 1], kdst1);
+      if (u + 1 < n1) dma(vb, rowtab[1][1][(u + 1) & 1], vdst1);
+      if (wave == 4 && u + 3 < n0) resolve(rowtab[0][0][(u + 1) & 1], 2 * (u + 3));
+      if (wave == 5 && u + 2 < n0) resolve(rowtab[0][1][u & 1], 2 * (u + 2));
+      if (wave == 6 && u + 3 < n1) resolve(rowtab[1][0][(u + 1) & 1], 2 * (u + 3) + 1);
+      if (wave == 7 && u + 2 < n1) resolve(rowtab[1][1][u & 1], 2 * (u + 2) + 1);
+    };
+    if (wave == 4) {
+      resolve(rowtab[0][0][0], 0);
+      if (n0 > 1) resolve(rowtab[0][0][1], 2);
+    }
+    if (wave == 5) {
+      resolve(rowtab[0][1][0], 0);
+      if (n0 > 1) resolve(rowtab[0][1][1], 2);
+    }
+    if (wave == 6 && n1 > 0) {
+      resolve(rowtab[1][0][0], 1);
+      if (n1 > 1) resolve(rowtab[1][0][1], 3);
+    }
+    if (wave == 7 && n1 > 0) {
+      resolve(rowtab[1][1][0], 1);
+      if (n1 > 1) resolve(rowtab[1][1][1], 3);
     }
     __syncthreads();
-    if (!group_b) {
-      if (active && t + 1 < ntiles) vphase(t + 1);
-    } else {
-      if (active) mphase(t, v_s0, k_s1);
+    if (group_b) {
+      dma(kb, rowtab[0][0][0], k_s0);
+      dma(vb, rowtab[0][1][0], v_s0);
+      if (n0 > 1) dma(kb, rowtab[0][0][1], k_s1);
+      if (n1 > 0) {
+        dma(kb, rowtab[1][0][0], k1_s0);
+        dma(vb, rowtab[1][1][0], v1_s0);
+        if (n1 > 1) dma(kb, rowtab[1][0][1], k1_s1);
+      }
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
-    if (t + 1 >= ntiles) break;
-    // tile t+1 (odd): V(t+1) in v_s1, K(t+2) in k_s0
-    if (!group_b) {
-      if (active) mphase(t + 1, v_s1, k_s0);
-    } else {
-      fetch(t + 1, k_s1, v_s0);
-      if (active) vphase(t + 1);
+    if (active) {
+      if (!group_b) {
+        scores(k_s0);
+        vphase(0);
+      } else if (n1 > 0) {
+        scores(k1_s0);
+      }
+    }
+    if (wave == 4 && n0 > 2) resolve(rowtab[0][0][0], 4);
+    if (wave == 6 && n1 > 2) resolve(rowtab[1][0][0], 5);
+    __syncthreads();
+    //   A: h = 2u -> M(u), h = 2u+1 -> V(u+1) on stream 0;  B: h = 2u -> V(u) + fetch, h = 2u+1 -> M(u)
+    //   on stream 1.  Group B runs out of tiles first (n1 <= n0) and then only fetches.
+    for (int u = 0; u < n0; u += 2) {
+      if (!group_b) {
+        if (active) mphase(u, v_s0, k_s1);
+      } else {
+        fetch2(u, k_s0, v_s1, k1_s0, v1_s1);
+        if (active && u < n1) vphase(2 * u + 1);
+      }
+      __syncthreads();
+      if (!group_b) {
+        if (active && u + 1 < n0) vphase(2 * u + 2);
+      } else {
+        if (active && u < n1) mphase(u, v1_s0, k1_s1);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __syncthreads();
+      if (u + 1 >= n0) break;
+      if (!group_b) {
+        if (active) mphase(u + 1, v_s1, k_s0);
+      } else {
+        fetch2(u + 1, k_s1, v_s0, k1_s1, v1_s0);
+        if (active && u + 1 < n1) vphase(2 * u + 3);
+      }
+      __syncthreads();
+      if (!group_b) {
+        if (active && u + 2 < n0) vphase(2 * u + 4);
+      } else {
+        if (active && u + 1 < n1) mphase(u + 1, v1_s1, k1_s0);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __syncthreads();
+    }
+    // Merge: group B leaves (m, l, O) in the stream-0 buffers (no tile is read any more and no copy
+    // is in flight); group A rescales both states to the common maximum and adds them.  Layout
+    // [db][r / 4][wave][lane] of 16-byte chunks for O, [wave][lane] of (m, l) pairs.
+    float* ob_lds[4] = {(float*)k_s0, (float*)k_s1, (float*)v_s0, (float*)v_s1};
+    float2* ml_lds = (float2*)k1_s0;
+    const int slot = wg * kWave + lane;
+    if (group_b && active) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          ((f32x4_t*)ob_lds[db])[r4 * 256 + slot] =
+              f32x4_t{acc[db][4 * r4], acc[db][4 * r4 + 1], acc[db][4 * r4 + 2], acc[db][4 * r4 + 3]};
+      ml_lds[slot] = make_float2(m_run, l_run);
     }
     __syncthreads();
-    if (!group_b) {
-      if (active && t + 2 < ntiles) vphase(t + 2);
-    } else {
-      if (active) mphase(t + 1, v_s1, k_s0);
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (group_b) return;
+    if (active) {
+      const float2 mlb = ml_lds[slot];
+      const float m = fmaxf(m_run, mlb.x);
+      // stream 0 holds tile 0, so m is finite; an empty stream 1 has m = -inf and weight 0
+      const float wa = __builtin_amdgcn_exp2f(m_run - m), wb = __builtin_amdgcn_exp2f(mlb.x - m);
+      l_run = l_run * wa + mlb.y * wb;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4_t o2 = ((const f32x4_t*)ob_lds[db])[r4 * 256 + slot];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[db][4 * r4 + e] = acc[db][4 * r4 + e] * wa + o2[e] * wb;
+        }
     }
-    __syncthreads();
   }
 
   if (!active) return;
@@ -664,7 +803,8 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   SVOO_REQUIRE((long long)bh * s * 128 < (1ll << 40), SVOO_ERR_UNSUPPORTED, "%s: too large", name);
   SVOO_REQUIRE(s < (1 << 24), SVOO_ERR_UNSUPPORTED, "%s: S=%d above 2^24 tokens per head", name, s);
   const VbsaWs lay = vbsa_layout(bh, s, qn, kn);
-  SVOO_REQUIRE(lay.cap < 65536, SVOO_ERR_UNSUPPORTED, "%s: too many q tiles per head", name);
+  // the tile index of a work item is 15 bits (bit 15 flags a half item)
+  SVOO_REQUIRE(lay.cap < 32768, SVOO_ERR_UNSUPPORTED, "%s: too many q tiles per head", name);
   SVOO_REQUIRE(workspace && ws_bytes >= lay.total, SVOO_ERR_WORKSPACE, "%s: workspace %zu < %zu", name, ws_bytes,
                lay.total);
   if (EAR) {
@@ -684,17 +824,25 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   int32_t* items = (int32_t*)(base + lay.items);
   int32_t* nitems = (int32_t*)(base + lay.nitems);
   constexpr int qtile = VbsaCfg<kDefaultQB>::kQTile;
+  const size_t smem = (size_t)((EAR ? 4 : 2) * kn + 1) * sizeof(int32_t);
+  // Half items need the kernel with a second set of K/V buffers (130 KB of static LDS with the row
+  // tables), which leaves 28 KB of the 160 KB LDS for the segment tables.
+  const bool half_ok = smem <= (size_t)28 * 1024;
   hipLaunchKernelGGL(vbsa_plan_kernel, dim3(bh), dim3(kPlanThreads), 0, st, q_sizes, k_sizes, s, qn, kn, qtile, lay.cap,
-                     qoff, koff, items, nitems, status);
+                     half_ok ? 1 : 0, qoff, koff, items, nitems, status);
   if (int rc = check_launch(name)) return rc;
   const long long total_items = (long long)bh * lay.cap;
   const long long nblocks = (total_items + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
   SVOO_REQUIRE(nblocks < (1ll << 31), SVOO_ERR_UNSUPPORTED, "%s: too many work items", name);
   const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)d));
-  const size_t smem = (size_t)((EAR ? 4 : 2) * kn + 1) * sizeof(int32_t);
-  hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX>), dim3((unsigned)nblocks), dim3(kVWaves * kWave), smem,
-                     st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items, nitems,
-                     scale_log2, q_idx, k_idx, heads);
+  if (half_ok)
+    hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX, true>), dim3((unsigned)nblocks), dim3(kVWaves * kWave),
+                       smem, st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items,
+                       nitems, scale_log2, q_idx, k_idx, heads);
+  else
+    hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX, false>), dim3((unsigned)nblocks), dim3(kVWaves * kWave),
+                       smem, st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items,
+                       nitems, scale_log2, q_idx, k_idx, heads);
   return check_launch(name);
 }
 }  // namespace

@@ -233,6 +233,50 @@ def test_vbsa_matches_oracle(gpu, h, qn, kn, s, density, seed):
     assert torch.all(out[0, 0, :a] == 0)
 
 
+@pytest.mark.parametrize("ear,kn", [(False, 24), (True, 24), (True, 2000)])
+def test_vbsa_half_items_match_oracle(gpu, ear, kn):
+    """Query clusters whose last 256-query tile holds at most 128 queries (the kernel splits such a
+    tile's KV stream over its two wave groups and merges the two softmax states), for KV streams of
+    1 to several 64-key tiles.  kn = 2000 with EAR leaves no LDS for the second stream: the same
+    sizes then run as full items."""
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd
+    from svoo_amd.ear import dynamic_block_sparse_prune_fwd
+
+    say("vbsa half items", "ear" if ear else "sap", kn)
+    h = 2
+    qsz = np.array([1, 31, 32, 33, 100, 128, 129, 255, 256, 257, 300, 384, 385, 640, 700], np.int32)
+    s = int(qsz.sum())
+    r = np.random.default_rng(40 + kn)
+    qs = np.stack([qsz, qsz[::-1]])[None]
+    cuts = np.sort(np.stack([r.choice(np.arange(1, s), size=kn - 1, replace=False) for _ in range(h)]), axis=1)
+    ks = np.diff(np.concatenate([np.zeros((h, 1), int), cuts, np.full((h, 1), s)], axis=1), axis=1).astype(np.int32)
+    ks = ks[None]
+    qn = len(qsz)
+    m = np.zeros((1, h, qn, kn), bool)
+    for b in range(h):
+        small = int(np.argmin(ks[0, b]))
+        for i in range(qn):
+            mode = (i + b) % 5
+            if mode == 0:
+                m[0, b, i, small] = True  # one short cluster: a single KV tile
+            else:
+                m[0, b, i] = r.random(kn) < (0.05, 0.15, 0.4, 1.0)[mode - 1]
+                m[0, b, i, small] = True
+    q, qt = rand_bf16((1, h, s, 128), 41, gpu, 0.5)
+    k, kt = rand_bf16((1, h, s, 128), 42, gpu, 0.5)
+    v, vt = rand_bf16((1, h, s, 128), 43, gpu)
+    mt, qst, kst = torch.from_numpy(m).to(gpu), torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu)
+    if ear:
+        kc, kct = rand_bf16((1, h, kn, 128), 44, gpu, 0.5)
+        vc, vct = rand_bf16((1, h, kn, 128), 45, gpu)
+        out = dynamic_block_sparse_prune_fwd(qt, kt, vt, kct, vct, mt, qst, kst)
+        ref = O.ear_compensated_attention(q, k, v, kc, vc, m, qs, ks)
+    else:
+        out = dynamic_block_sparse_fwd(qt, kt, vt, mt, qst, kst)
+        ref = O.block_sparse_attention(q, k, v, m, qs, ks)
+    _attn_check(out, ref)
+
+
 def test_vbsa_dense_equals_sdpa(gpu):
     from svoo_amd.co_clustering import dynamic_block_sparse_fwd
 
