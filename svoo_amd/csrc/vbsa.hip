@@ -274,7 +274,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   // IDX: sorted position -> token row of this head, and the output row of a sorted query position
   const int32_t* qix = IDX ? q_idx + (size_t)b * s : nullptr;
   const int32_t* kix = IDX ? k_idx + (size_t)b * s : nullptr;
-  auto out_row = [&](int r) -> uint16_t* {
+  auto out_row = [&](int r) __attribute__((always_inline)) -> uint16_t* {
     if constexpr (IDX)
       return o + (((size_t)(b / heads) * s + qix[r]) * heads + (b % heads)) * 128;
     else
@@ -340,7 +340,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   if ((wave == 4 || wave == 5 || (half && wave >= 6)) && nseg > 0)
     cursor_init(cursor, seg_start, seg_cum, nseg, min((wave >= 6 ? kKT : 0) + lane, total_tok - 1));
   const int crow = (wave & 1) ? crow_v : crow_k;  // the resolving waves: even for K, odd for V
-  auto resolve = [&](int32_t* tab, int t) {
+  auto resolve = [&](int32_t* tab, int t) __attribute__((always_inline)) {
     const int p = t * kKT + lane;
     if (p < total_tok) {
       const int pos = cursor_row(cursor, seg_start, seg_cum, p);
@@ -353,7 +353,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   };
   // DMA mapping (group B): wave 4+w, group j moves tile rows 4(kDmaIt w + j) + lane/16.
   const int prow = lane / 16, pch = lane % 16;
-  auto dma = [&](const uint16_t* src, const int32_t* tab, uint16_t* buf) {
+  auto dma = [&](const uint16_t* src, const int32_t* tab, uint16_t* buf) __attribute__((always_inline)) {
     int rows[kDmaIt];  // all table reads first: one LDS wait for the group
 #pragma unroll
     for (int j = 0; j < kDmaIt; ++j) rows[j] = tab[4 * (kDmaIt * wg + j) + prow];
@@ -369,6 +369,28 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
         lds_dma16((const char*)src + off, buf + 4 * (kDmaIt * wg + j) * 128);
       }
     }
+  };
+  // The same copies one group at a time (full items: interleaved with group B's softmax), with the
+  // wave's four table rows read ahead into registers.
+  auto dma_rows = [&](const int32_t* tab) __attribute__((always_inline)) -> int4 {
+    const int o = 4 * kDmaIt * wg + prow;
+    return make_int4(tab[o], tab[o + 4], tab[o + 8], tab[o + 12]);
+  };
+  auto dma_one = [&](const uint16_t* src, int row, int j, uint16_t* buf) __attribute__((always_inline)) {
+    const int r = 4 * (kDmaIt * wg + j) + prow;
+    if constexpr (EAR) {
+      lds_dma16(src + (long long)row * 128 + swz(r, pch) * 8, buf + 4 * (kDmaIt * wg + j) * 128);
+    } else {
+      const uint32_t off = (uint32_t)row * 256u + (uint32_t)swz(r, pch) * 16u;
+      lds_dma16((const char*)src + off, buf + 4 * (kDmaIt * wg + j) * 128);
+    }
+  };
+  auto dma_all = [&](int4 rk4, uint16_t* kdst, int4 rv4, uint16_t* vdst) __attribute__((always_inline)) {
+    const int rka[4] = {rk4.x, rk4.y, rk4.z, rk4.w}, rva[4] = {rv4.x, rv4.y, rv4.z, rv4.w};
+#pragma unroll
+    for (int j = 0; j < kDmaIt; ++j) dma_one(kb, rka[j], j, kdst);
+#pragma unroll
+    for (int j = 0; j < kDmaIt; ++j) dma_one(vb, rva[j], j, vdst);
   };
 
   int koffs[8], voffs[2][4];
@@ -388,7 +410,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   f32x16_t sacc[2];
   u32x4_t pop[2][2];
 
-  auto scores = [&](const uint16_t* kt) {
+  auto scores = [&](const uint16_t* kt) __attribute__((always_inline)) {
     sacc[0] = f32x16_t{};
     sacc[1] = f32x16_t{};
 #pragma unroll
@@ -403,7 +425,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   // MFMA phase M(t): O += V(t)^T P(t)^T, then S(t+1).  The 32 MFMAs run as one software pipeline whose
   // operand reads are issued two MFMAs ahead into three rotating buffers (the order is pinned with
   // scheduling barriers).  S(t+1) is also computed after the last tile, on stale LDS, and not used.
-  auto mop = [&](int i, const uint16_t* vt, const uint16_t* knext) -> u32x4_t {
+  auto mop = [&](int i, const uint16_t* vt, const uint16_t* knext) __attribute__((always_inline)) -> u32x4_t {
     if (i < 16) {
       const int kb2 = i / 8, st = (i / 4) % 2, db = i % 4;
       const int rb = (kb2 * 32 + st * 16) * 128;
@@ -414,12 +436,12 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     const int j = i - 16, ks2 = j / 2, kb2 = j % 2;
     return *(const u32x4_t*)(&knext[kb2 * 32 * 128 + koffs[ks2]]);
   };
-  auto mphase = [&](int t, const uint16_t* vt, const uint16_t* knext) {
+  auto mphase = [&](int t, const uint16_t* vt, const uint16_t* knext) __attribute__((always_inline)) {
     u32x4_t buf[3];
     buf[0] = mop(0, vt, knext);
     buf[1] = mop(1, vt, knext);
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-    auto mm = [&](int i) {
+    auto mm = [&](int i) __attribute__((always_inline)) {
       if (i < 16) {
         const int kb2 = i / 8, st = (i / 4) % 2, db = i % 4;
         acc[db] = mfma32x32x16(as_bf16x8(buf[i % 3]), as_bf16x8(pop[kb2][st]), acc[db]);
@@ -447,8 +469,11 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     mm(31);
     (void)t;
   };
-  // VALU phase V(t): online softmax of S(t) -> bf16 P(t) (per lane: one query, 32 of 64 keys).
-  auto vphase = [&](int t) {
+  // VALU phase V(t): online softmax of S(t) -> bf16 P(t) (per lane: one query, 32 of 64 keys).  With
+  // dmaon the eight copy groups of this wave (rows rk4 into kdst, rv4 into vdst) are issued between the
+  // exponentials, one per four scores, so the vector-memory path sees them spread over the phase.
+  auto vphase = [&](int t, bool dmaon = false, int4 rk4 = int4{}, uint16_t* kdst = nullptr, int4 rv4 = int4{},
+                    uint16_t* vdst = nullptr) __attribute__((always_inline)) {
     // sl: the factor from sacc to log2-domain logits (1 once an EAR tile is pre-scaled and biased)
     float sl = scale_log2;
     if constexpr (EAR) {
@@ -480,13 +505,53 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
           }
       }
     }
-    float mx = sacc[0][0];
+    // P against the running max m_run.  The lane's row sum over its 32 values bounds each of them, so
+    // the maximum is only needed when the sum leaves [0, 2^13]: a value more than 13 (log2) above
+    // m_run, or the first tile (m_run = -inf gives inf / NaN).  Then m_run moves to the tile maximum,
+    // O and l are rescaled and P is recomputed.
+    const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+    auto pexp = [&](bool dm) __attribute__((always_inline)) -> float {
+      const float mneg = -m_run;
+      const int rka[4] = {rk4.x, rk4.y, rk4.z, rk4.w}, rva[4] = {rv4.x, rv4.y, rv4.z, rv4.w};
+      float ls0 = 0.0f, ls1 = 0.0f;
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2)
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+        float pv[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb2][r]);
-    mx = xhalf_max(mx) * sl;
-    if (__any(mx > m_run + 8.0f)) {
+        for (int r = 0; r < 16; ++r) {
+          pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][r], sl, mneg));
+          if (dm && r % 4 == 3) {
+            const int j = (kb2 * 16 + r) / 4;
+            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+            if (j < kDmaIt)
+              dma_one(kb, rka[j], j, kdst);
+            else
+              dma_one(vb, rva[j - kDmaIt], j - kDmaIt, vdst);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          }
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t w = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
+            pop[kb2][st][e] = w;
+            if (e & 1)
+              ls1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, ls1, false);
+            else
+              ls0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, ls0, false);
+          }
+      }
+      return ls0 + ls1;
+    };
+    float lsum = dmaon ? pexp(true) : pexp(false);
+    if (__any(!(lsum <= 8192.0f))) {
+      float mx = sacc[0][0];
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb2][r]);
+      mx = xhalf_max(mx) * sl;
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;
@@ -495,48 +560,22 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+      lsum = pexp(false);
     }
-    const float mneg = -m_run;
-    // The row sum adds the bf16 P pairs the PV MFMA consumes, two per v_dot2 with (1, 1).
-    const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
-    float ls0 = 0.0f, ls1 = 0.0f;
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-      float pv[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[kb2][r], sl, mneg));
-#pragma unroll
-      for (int st = 0; st < 2; ++st)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t w = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
-          pop[kb2][st][e] = w;
-          if (e & 1)
-            ls1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, ls1, false);
-          else
-            ls0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, ls0, false);
-        }
-    }
-    l_run += ls0 + ls1;
+    l_run += lsum;
   };
-  // Group B housekeeping at the start of its V(t): DMA K(t+2), V(t+1); resolve K(t+3), V(t+2).
-  auto fetch = [&](int t, uint16_t* kdst, uint16_t* vdst) {
-    if (t + 2 < ntiles) dma(kb, rowtab[0][0][t & 1], kdst);
-    if (t + 1 < ntiles) dma(vb, rowtab[0][1][(t + 1) & 1], vdst);
-    if (wave == 4 && t + 3 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 3);
-    if (wave == 5 && t + 2 < ntiles) resolve(rowtab[0][1][t & 1], t + 2);
-  };
-
   if (!half) {
-    // Prologue: tables K(0), K(1), V(0), V(1); DMA K(0), V(0) -> buffers 0, K(1) -> K buffer 1;
-    // S(0) everywhere, V(0) in group A; table K(2).
+    // Prologue: tables K(0), K(1), V(0), V(1) (a table past the stream holds the last row, so copies
+    // of tiles past the end stay inside this head); DMA K(0), V(0) -> buffers 0, K(1) -> K buffer 1;
+    // S(0) everywhere, V(0) in group A; tables K(2), K(3), V(2); group B reads the rows of its first
+    // copies (K(2), V(1)).
     if (wave == 4) {
       resolve(rowtab[0][0][0], 0);
-      if (ntiles > 1) resolve(rowtab[0][0][1], 1);
+      resolve(rowtab[0][0][1], 1);
     }
     if (wave == 5) {
       resolve(rowtab[0][1][0], 0);
-      if (ntiles > 1) resolve(rowtab[0][1][1], 1);
+      resolve(rowtab[0][1][1], 1);
     }
     __syncthreads();
     if (group_b) {
@@ -548,24 +587,43 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     __syncthreads();
     if (active) scores(k_s0);
     if (active && !group_b) vphase(0);
-    if (wave == 4 && ntiles > 2) resolve(rowtab[0][0][0], 2);
+    if (wave == 4) {
+      resolve(rowtab[0][0][0], 2);
+      resolve(rowtab[0][0][1], 3);
+    }
+    if (wave == 5) resolve(rowtab[0][1][0], 2);
     __syncthreads();
+    int4 rk = make_int4(0, 0, 0, 0), rv = make_int4(0, 0, 0, 0);
+    if (group_b) {
+      rk = dma_rows(rowtab[0][0][0]);
+      rv = dma_rows(rowtab[0][1][1]);
+    }
 
     // Half-steps h = 0 .. 2T-1 (unrolled by 4: tile parity fixes the buffers).
-    //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1)        B: h = 2t -> V(t) + fetch;  h = 2t+1 -> M(t)
+    //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1)
+    //   B: h = 2t -> V(t) with the copies of K(t+2) and V(t+1) spread through it;
+    //      h = 2t+1 -> M(t), tables K(t+4) and V(t+3) (waves 4, 5), rows of the next copies, wait for
+    //      the copies.
+    // Copies run for tiles past the end too (rows from the tables), so the phases carry no branches.
     for (int t = 0; t < ntiles; t += 2) {
       // tile t (even): V(t) in v_s0, K(t+1) in k_s1
       if (!group_b) {
         if (active) mphase(t, v_s0, k_s1);
       } else {
-        fetch(t, k_s0, v_s1);
-        if (active) vphase(t);
+        if (active)
+          vphase(t, true, rk, k_s0, rv, v_s1);
+        else
+          dma_all(rk, k_s0, rv, v_s1);
       }
       __syncthreads();
       if (!group_b) {
         if (active && t + 1 < ntiles) vphase(t + 1);
       } else {
         if (active) mphase(t, v_s0, k_s1);
+        if (wave == 4 && t + 4 < ntiles) resolve(rowtab[0][0][t & 1], t + 4);
+        if (wave == 5 && t + 3 < ntiles) resolve(rowtab[0][1][(t + 1) & 1], t + 3);
+        rk = dma_rows(rowtab[0][0][(t + 1) & 1]);
+        rv = dma_rows(rowtab[0][1][t & 1]);
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       __syncthreads();
@@ -574,14 +632,20 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       if (!group_b) {
         if (active) mphase(t + 1, v_s1, k_s0);
       } else {
-        fetch(t + 1, k_s1, v_s0);
-        if (active) vphase(t + 1);
+        if (active)
+          vphase(t + 1, true, rk, k_s1, rv, v_s0);
+        else
+          dma_all(rk, k_s1, rv, v_s0);
       }
       __syncthreads();
       if (!group_b) {
         if (active && t + 2 < ntiles) vphase(t + 2);
       } else {
         if (active) mphase(t + 1, v_s1, k_s0);
+        if (wave == 4 && t + 5 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 5);
+        if (wave == 5 && t + 4 < ntiles) resolve(rowtab[0][1][t & 1], t + 4);
+        rk = dma_rows(rowtab[0][0][t & 1]);
+        rv = dma_rows(rowtab[0][1][(t + 1) & 1]);
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       __syncthreads();
@@ -591,7 +655,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     // k_s / v_s buffers and is used by group A, stream 1 (n1 tiles) in k1_s / v1_s, used by group B.
     // Group B fetches both streams with the full item's timing; waves 4-7 resolve the four tables.
     const int n0 = (ntiles + 1) / 2, n1 = ntiles / 2;
-    auto fetch2 = [&](int u, uint16_t* kdst0, uint16_t* vdst0, uint16_t* kdst1, uint16_t* vdst1) {
+    auto fetch2 = [&](int u, uint16_t* kdst0, uint16_t* vdst0, uint16_t* kdst1, uint16_t* vdst1) __attribute__((always_inline)) {
       if (u + 2 < n0) dma(kb, rowtab[0][0][u & 1], kdst0);
       if (u + 1 < n0) dma(vb, rowtab[0][1][(u + 1) & 1], vdst0);
       if (u + 2 < n1) dma(kb, rowtab[1][0][u & 1], kdst1);
@@ -826,8 +890,9 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   constexpr int qtile = VbsaCfg<kDefaultQB>::kQTile;
   const size_t smem = (size_t)((EAR ? 4 : 2) * kn + 1) * sizeof(int32_t);
   // Half items need the kernel with a second set of K/V buffers (130 KB of static LDS with the row
-  // tables), which leaves 28 KB of the 160 KB LDS for the segment tables.
-  const bool half_ok = smem <= (size_t)28 * 1024;
+  // tables), which leaves 28 KB of the 160 KB LDS for the segment tables.  The EAR kernel (64-bit copy
+  // addresses for the centroid rows) runs full items only: with both paths it exceeds 256 registers.
+  const bool half_ok = !EAR && smem <= (size_t)28 * 1024;
   hipLaunchKernelGGL(vbsa_plan_kernel, dim3(bh), dim3(kPlanThreads), 0, st, q_sizes, k_sizes, s, qn, kn, qtile, lay.cap,
                      half_ok ? 1 : 0, qoff, koff, items, nitems, status);
   if (int rc = check_launch(name)) return rc;
@@ -835,8 +900,8 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   const long long nblocks = (total_items + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
   SVOO_REQUIRE(nblocks < (1ll << 31), SVOO_ERR_UNSUPPORTED, "%s: too many work items", name);
   const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)d));
-  if (half_ok)
-    hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX, true>), dim3((unsigned)nblocks), dim3(kVWaves * kWave),
+  if (!EAR && half_ok)
+    hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX, !EAR>), dim3((unsigned)nblocks), dim3(kVWaves * kWave),
                        smem, st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items,
                        nitems, scale_log2, q_idx, k_idx, heads);
   else
