@@ -508,12 +508,12 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     // P against the running max m_run.  The lane's row sum over its 32 values bounds each of them, so
     // the maximum is only needed when the sum leaves [0, 2^13]: a value more than 13 (log2) above
     // m_run, or the first tile (m_run = -inf gives inf / NaN).  Then m_run moves to the tile maximum,
-    // O and l are rescaled and P is recomputed.
-    const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+    // O and l are rescaled and P is recomputed.  The row sum adds the fp32 values (as the reference's
+    // kernel does) in four chains.
     auto pexp = [&](bool dm) __attribute__((always_inline)) -> float {
       const float mneg = -m_run;
       const int rka[4] = {rk4.x, rk4.y, rk4.z, rk4.w}, rva[4] = {rv4.x, rv4.y, rv4.z, rv4.w};
-      float ls0 = 0.0f, ls1 = 0.0f;
+      float la[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2) {
         float pv[16];
@@ -533,16 +533,11 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t w = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
-            pop[kb2][st][e] = w;
-            if (e & 1)
-              ls1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, ls1, false);
-            else
-              ls0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), ones, ls0, false);
-          }
+          for (int e = 0; e < 4; ++e) pop[kb2][st][e] = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) la[r % 4] += pv[r];
       }
-      return ls0 + ls1;
+      return (la[0] + la[1]) + (la[2] + la[3]);
     };
     float lsum = dmaon ? pexp(true) : pexp(false);
     if (__any(!(lsum <= 8192.0f))) {
