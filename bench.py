@@ -58,6 +58,9 @@ def parse_args():
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU baseline sample")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "vbsa_attn_C3_traffic.json"),
                     help="measured HBM traffic of the attention kernel (from rocprofv3 --pmc), if present")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run three 1 GiB device copies (the known-size reference for rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE scaling) and exit")
     return ap.parse_args()
 
 
@@ -81,6 +84,16 @@ def main():
               "a single MI355X (multi-GPU sharding is design-only); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    if args.copy_calibration:
+        import torch
+
+        src = torch.empty((1 << 30) // 2, dtype=torch.bfloat16, device="cuda:0").normal_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("three 1 GiB copies done")
+        return
     if args.config == "C5":
         return main_dit(args)
     if args.sparsity_profile:

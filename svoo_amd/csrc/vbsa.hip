@@ -330,14 +330,14 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   for (int db = 0; db < 4; ++db) acc[db] = f32x16_t{};
   float m_run = -INFINITY, l_run = 0.0f;
 
-  // Row tables: wave 4 resolves K tiles, wave 5 V tiles (lane = tile position); in a half item waves 4
-  // and 5 resolve stream 0 (even tiles), waves 6 and 7 stream 1 (odd tiles).
+  // Row tables (lane = tile position): in a full item wave 0 resolves K tiles and wave 1 V tiles; in a
+  // half item waves 4 and 5 resolve stream 0 (even tiles), waves 6 and 7 stream 1 (odd tiles).
   // Rows past the stream repeat its last token row (0 when an EAR row has no active tokens); EAR
   // centroid j of the K (V) table is row crow_k + j (crow_v + j).
   int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
   if constexpr (IDX) last_row = kix[last_row];
   KvCursor cursor;
-  if ((wave == 4 || wave == 5 || (half && wave >= 6)) && nseg > 0)
+  if ((half ? wave >= 4 : wave < 2) && nseg > 0)
     cursor_init(cursor, seg_start, seg_cum, nseg, min((wave >= 6 ? kKT : 0) + lane, total_tok - 1));
   const int crow = (wave & 1) ? crow_v : crow_k;  // the resolving waves: even for K, odd for V
   auto resolve = [&](int32_t* tab, int t) __attribute__((always_inline)) {
@@ -564,11 +564,11 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     // of tiles past the end stay inside this head); DMA K(0), V(0) -> buffers 0, K(1) -> K buffer 1;
     // S(0) everywhere, V(0) in group A; tables K(2), K(3), V(2); group B reads the rows of its first
     // copies (K(2), V(1)).
-    if (wave == 4) {
+    if (wave == 0) {
       resolve(rowtab[0][0][0], 0);
       resolve(rowtab[0][0][1], 1);
     }
-    if (wave == 5) {
+    if (wave == 1) {
       resolve(rowtab[0][1][0], 0);
       resolve(rowtab[0][1][1], 1);
     }
@@ -582,11 +582,11 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     __syncthreads();
     if (active) scores(k_s0);
     if (active && !group_b) vphase(0);
-    if (wave == 4) {
+    if (wave == 0) {
       resolve(rowtab[0][0][0], 2);
       resolve(rowtab[0][0][1], 3);
     }
-    if (wave == 5) resolve(rowtab[0][1][0], 2);
+    if (wave == 1) resolve(rowtab[0][1][0], 2);
     __syncthreads();
     int4 rk = make_int4(0, 0, 0, 0), rv = make_int4(0, 0, 0, 0);
     if (group_b) {
@@ -595,10 +595,9 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     }
 
     // Half-steps h = 0 .. 2T-1 (unrolled by 4: tile parity fixes the buffers).
-    //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1)
+    //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1), tables K(t+4) and V(t+3) (waves 0, 1)
     //   B: h = 2t -> V(t) with the copies of K(t+2) and V(t+1) spread through it;
-    //      h = 2t+1 -> M(t), tables K(t+4) and V(t+3) (waves 4, 5), rows of the next copies, wait for
-    //      the copies.
+    //      h = 2t+1 -> M(t), rows of the next copies K(t+3) and V(t+2), wait for the copies.
     // Copies run for tiles past the end too (rows from the tables), so the phases carry no branches.
     for (int t = 0; t < ntiles; t += 2) {
       // tile t (even): V(t) in v_s0, K(t+1) in k_s1
@@ -613,10 +612,10 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       __syncthreads();
       if (!group_b) {
         if (active && t + 1 < ntiles) vphase(t + 1);
+        if (wave == 0 && t + 4 < ntiles) resolve(rowtab[0][0][t & 1], t + 4);
+        if (wave == 1 && t + 3 < ntiles) resolve(rowtab[0][1][(t + 1) & 1], t + 3);
       } else {
         if (active) mphase(t, v_s0, k_s1);
-        if (wave == 4 && t + 4 < ntiles) resolve(rowtab[0][0][t & 1], t + 4);
-        if (wave == 5 && t + 3 < ntiles) resolve(rowtab[0][1][(t + 1) & 1], t + 3);
         rk = dma_rows(rowtab[0][0][(t + 1) & 1]);
         rv = dma_rows(rowtab[0][1][t & 1]);
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -635,10 +634,10 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       __syncthreads();
       if (!group_b) {
         if (active && t + 2 < ntiles) vphase(t + 2);
+        if (wave == 0 && t + 5 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 5);
+        if (wave == 1 && t + 4 < ntiles) resolve(rowtab[0][1][t & 1], t + 4);
       } else {
         if (active) mphase(t + 1, v_s1, k_s0);
-        if (wave == 4 && t + 5 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 5);
-        if (wave == 5 && t + 4 < ntiles) resolve(rowtab[0][1][t & 1], t + 4);
         rk = dma_rows(rowtab[0][0][t & 1]);
         rv = dma_rows(rowtab[0][1][(t + 1) & 1]);
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
