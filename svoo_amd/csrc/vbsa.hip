@@ -41,7 +41,9 @@ struct VbsaCfg {
 
 // ------------------------------------------------------------------------------------------ plan
 __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* __restrict__ qs,
-                                                                 const int32_t* __restrict__ ks, int s, int qn, int kn,
+                                                                 const int32_t* __restrict__ ks,
+                                                                 const uint8_t* __restrict__ map, int ear,
+                                                                 int32_t* __restrict__ work, int s, int qn, int kn,
                                                                  int qtile, int cap, int half_ok,
                                                                  int32_t* __restrict__ qoff,
                                                                  int32_t* __restrict__ koff,
@@ -111,6 +113,51 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
       nitems[b] = ok ? (int32_t)(tot >> 32) : 0;
       if (!ok && status) atomicOr(status, 1);
     }
+  }
+  // Work of the head in KV tiles (the attention's launch order runs heavy heads first): one wave per
+  // query cluster sums the stream length of its map row (active keys, plus the inactive centroids for
+  // EAR) and weighs it by the cluster's query tiles.
+  {
+    const int wave = tid / kWave, lane = tid % kWave;
+    long long wsum = 0;
+    for (int i = wave; i < qn; i += kPlanThreads / kWave) {
+      const uint8_t* mrow = map + ((size_t)b * qn + i) * kn;
+      int act = 0;
+      for (int j = lane; j < kn; j += kWave) act += mrow[j] ? ksb[j] : ear;
+#pragma unroll
+      for (int o = kWave / 2; o > 0; o >>= 1) act += __shfl_xor(act, o);
+      const int v = qsb[i];
+      if (v > 0) wsum += (long long)((v + qtile - 1) / qtile) * (1 + (act + kKT - 1) / kKT);
+    }
+    __syncthreads();  // the scans above are done with red
+    if (lane == 0) red[wave] = wsum;
+    __syncthreads();
+    if (tid == 0) {
+      long long w = 0;
+      for (int i = 0; i < kPlanThreads / kWave; ++i) w += red[i];
+      work[b] = (int32_t)min(w, 0x7fffffffll);
+    }
+  }
+}
+
+// Launch order of the heads: by work, heaviest first (ties by index), so the last work items of the
+// grid are short ones.  bh above kOrderMax keeps the natural order.
+constexpr int kOrderMax = 4096;
+__global__ void __launch_bounds__(kPlanThreads) vbsa_order_kernel(const int32_t* __restrict__ work, int bh,
+                                                                  int32_t* __restrict__ order) {
+  __shared__ int32_t w[kOrderMax];
+  const int tid = threadIdx.x;
+  if (bh > kOrderMax) {
+    for (int h = tid; h < bh; h += kPlanThreads) order[h] = h;
+    return;
+  }
+  for (int h = tid; h < bh; h += kPlanThreads) w[h] = work[h];
+  __syncthreads();
+  for (int h = tid; h < bh; h += kPlanThreads) {
+    const int wh = w[h];
+    int rank = 0;
+    for (int g = 0; g < bh; ++g) rank += (w[g] > wh || (w[g] == wh && g < h)) ? 1 : 0;
+    order[rank] = h;
   }
 }
 
@@ -238,7 +285,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     const uint8_t* __restrict__ map, const int32_t* __restrict__ ks, uint16_t* __restrict__ o, int s, int qn, int kn,
     int cap, long long total_items, const int32_t* __restrict__ qoff, const int32_t* __restrict__ koff,
     const int32_t* __restrict__ items, const int32_t* __restrict__ nitems, float scale_log2,
-    const int32_t* __restrict__ q_idx, const int32_t* __restrict__ k_idx, int heads) {
+    const int32_t* __restrict__ q_idx, const int32_t* __restrict__ k_idx, int heads,
+    const int32_t* __restrict__ order) {
   constexpr int kQTile = VbsaCfg<QB>::kQTile;
   constexpr int kThreads = kVWaves * kWave;
   constexpr int kDmaIt = kKT / (4 * 4);  // 4-row DMA groups per group-B wave per tile and matrix
@@ -253,7 +301,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
 
   const long long item = xcd_item(blockIdx.x);
   if (item >= total_items) return;
-  const int b = (int)(item / cap), local = (int)(item % cap);
+  const int b = order[(int)(item / cap)], local = (int)(item % cap);
   if (local >= nitems[b]) return;
   const int packed = items[(size_t)b * cap + local];
   const int ci = packed >> 16, tile = packed & 0x7fff;
@@ -825,7 +873,7 @@ using namespace svoo;
 namespace {
 constexpr int kDefaultQB = 1;
 struct VbsaWs {
-  size_t qoff, koff, items, nitems, total;
+  size_t qoff, koff, items, nitems, work, order, total;
   int cap;
 };
 VbsaWs vbsa_layout(int bh, int s, int qn, int kn) {
@@ -837,7 +885,9 @@ VbsaWs vbsa_layout(int bh, int s, int qn, int kn) {
   w.koff = w.qoff + al((size_t)bh * (qn + 1) * 4);
   w.items = w.koff + al((size_t)bh * (kn + 1) * 4);
   w.nitems = w.items + al((size_t)bh * w.cap * 4);
-  w.total = w.nitems + al((size_t)bh * 4);
+  w.work = w.nitems + al((size_t)bh * 4);
+  w.order = w.work + al((size_t)bh * 4);
+  w.total = w.order + al((size_t)bh * 4);
   return w;
 }
 }  // namespace
@@ -881,14 +931,18 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   int32_t* koff = (int32_t*)(base + lay.koff);
   int32_t* items = (int32_t*)(base + lay.items);
   int32_t* nitems = (int32_t*)(base + lay.nitems);
+  int32_t* work = (int32_t*)(base + lay.work);
+  int32_t* order = (int32_t*)(base + lay.order);
   constexpr int qtile = VbsaCfg<kDefaultQB>::kQTile;
   const size_t smem = (size_t)((EAR ? 4 : 2) * kn + 1) * sizeof(int32_t);
   // Half items need the kernel with a second set of K/V buffers (130 KB of static LDS with the row
   // tables), which leaves 28 KB of the 160 KB LDS for the segment tables.  The EAR kernel (64-bit copy
   // addresses for the centroid rows) runs full items only: with both paths it exceeds 256 registers.
   const bool half_ok = !EAR && smem <= (size_t)28 * 1024;
-  hipLaunchKernelGGL(vbsa_plan_kernel, dim3(bh), dim3(kPlanThreads), 0, st, q_sizes, k_sizes, s, qn, kn, qtile, lay.cap,
-                     half_ok ? 1 : 0, qoff, koff, items, nitems, status);
+  hipLaunchKernelGGL(vbsa_plan_kernel, dim3(bh), dim3(kPlanThreads), 0, st, q_sizes, k_sizes, map, EAR ? 1 : 0, work,
+                     s, qn, kn, qtile, lay.cap, half_ok ? 1 : 0, qoff, koff, items, nitems, status);
+  if (int rc = check_launch(name)) return rc;
+  hipLaunchKernelGGL(vbsa_order_kernel, dim3(1), dim3(kPlanThreads), 0, st, work, bh, order);
   if (int rc = check_launch(name)) return rc;
   const long long total_items = (long long)bh * lay.cap;
   const long long nblocks = (total_items + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
@@ -897,11 +951,11 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   if (!EAR && half_ok)
     hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX, !EAR>), dim3((unsigned)nblocks), dim3(kVWaves * kWave),
                        smem, st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items,
-                       nitems, scale_log2, q_idx, k_idx, heads);
+                       nitems, scale_log2, q_idx, k_idx, heads, order);
   else
     hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX, false>), dim3((unsigned)nblocks), dim3(kVWaves * kWave),
                        smem, st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items,
-                       nitems, scale_log2, q_idx, k_idx, heads);
+                       nitems, scale_log2, q_idx, k_idx, heads, order);
   return check_launch(name);
 }
 }  // namespace
