@@ -258,7 +258,10 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
 // registers as the MFMA B operand for the whole pass.  E_hi and E_lo stream through LDS in chunks
 // of 64 rows, double buffered and filled by LDS DMA (unpadded rows, XOR-swizzled 16-byte chunks),
 // one barrier per chunk.  Each lane keeps a running argmax over the 16 cluster rows it holds of
-// each 32x32 accumulator tile; ties resolve to the lowest cluster index.
+// each 32x32 accumulator tile: one max over the scores with their slot in the low 4 mantissa bits,
+// then a tile-level compare (ties resolve to the lowest cluster index; scores within 2^-19 of each
+// other, below the rounding of the hi + lo sums, are ordered by slot, and for negative scores the
+// higher slot of a tile wins such a near-tie).
 constexpr int kAsgTokWave = 128;
 constexpr int kAsgTok = 4 * kAsgTokWave;
 
@@ -305,8 +308,9 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   const int abase = l32 * 128 + 8 * (h ^ (sw & 1));
 #define AOFF(ks) (abase + 16 * ((ks) ^ g))
 
-  float best_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  int best_j[4] = {0, 0, 0, 0};
+  float best_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // tagged
+  float best_s[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // without the tag
+  int best_j[4] = {0, 0, 0, 0};                                     // tile base row
 
   for (int c = 0; c < nchunks; ++c) {
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -335,30 +339,45 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma32x32x16(as_bf16x8(cl), as_bf16x8(xop[cb][ks]), acc[cb]);
       }
-      // Row of element r is jb + (r/4)*8 + r%4 + 4h; the lane term 4h is added once at the end,
-      // so the selected index is a wave-uniform constant.
+      // Argmax over the lane's 16 values of each tile: the low 4 mantissa bits of each score are
+      // replaced by 15 - r (a change of at most 2^-19 of the score, below the rounding of the hi + lo
+      // sums), so one max over the tagged values gives the tile's best score and, on equal scores, the
+      // lowest slot; across tiles the scores are compared without the tags (ties keep the earlier tile).
+      // Row of slot r is jb + (r/4)*8 + r%4 + 4h, decoded at the end.
       const int jb = c * kAssignChunk + rb * 32;
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
+        float t[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float v = acc[cb][r];
-          const bool up = v > best_v[cb];
-          best_v[cb] = fmaxf(v, best_v[cb]);
-          best_j[cb] = up ? jb + (r / 4) * 8 + (r % 4) : best_j[cb];
+        for (int r = 0; r < 16; ++r)
+        {
+          const float av = acc[cb][r];
+          t[r] = __uint_as_float((__float_as_uint(av) & ~15u) | (uint32_t)(15 - r));
         }
+        auto max3 = [](float a, float b, float c) { return fmaxf(fmaxf(a, b), c); };
+        const float m = fmaxf(max3(max3(t[0], t[1], t[2]), max3(t[3], t[4], t[5]), max3(t[6], t[7], t[8])),
+                              max3(max3(t[9], t[10], t[11]), max3(t[12], t[13], t[14]), t[15]));
+        const float ms = __uint_as_float(__float_as_uint(m) & ~15u);
+        const bool up = ms > best_s[cb];
+        best_s[cb] = up ? ms : best_s[cb];
+        best_v[cb] = up ? m : best_v[cb];
+        best_j[cb] = up ? jb : best_j[cb];
       }
     }
   }
 #undef AOFF
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) best_j[cb] += h * 4;
+  for (int cb = 0; cb < 4; ++cb) {
+    const int r = 15 - (int)(__float_as_uint(best_v[cb]) & 15u);
+    best_j[cb] += (r / 4) * 8 + (r % 4) + h * 4;
+  }
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
-    const float ov = __shfl_xor(best_v[cb], 32);
+    // the two halves of a token: larger score, then lower row
+    const float ov = __shfl_xor(best_s[cb], 32);
     const int oj = __shfl_xor(best_j[cb], 32);
-    if (ov > best_v[cb] || (ov == best_v[cb] && oj < best_j[cb])) {
-      best_v[cb] = ov;
+    if (ov > best_s[cb] || (ov == best_s[cb] && oj < best_j[cb])) {
+      best_s[cb] = ov;
       best_j[cb] = oj;
     }
     const int tok = tok0 + cb * 32 + l32;
