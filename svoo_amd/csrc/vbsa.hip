@@ -123,7 +123,12 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
     for (int i = wave; i < qn; i += kPlanThreads / kWave) {
       const uint8_t* mrow = map + ((size_t)b * qn + i) * kn;
       int act = 0;
-      for (int j = lane; j < kn; j += kWave) act += mrow[j] ? ksb[j] : ear;
+      // both loads unconditional and 16 iterations unrolled: the loads of a row are in flight together
+#pragma unroll 16
+      for (int j = lane; j < kn; j += kWave) {
+        const int kv = ksb[j], on = mrow[j];
+        act += on ? kv : ear;
+      }
 #pragma unroll
       for (int o = kWave / 2; o > 0; o >>= 1) act += __shfl_xor(act, o);
       const int v = qsb[i];
@@ -385,19 +390,33 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
   if constexpr (IDX) last_row = kix[last_row];
   KvCursor cursor;
-  if ((half ? wave >= 4 : wave < 2) && nseg > 0)
-    cursor_init(cursor, seg_start, seg_cum, nseg, min((wave >= 6 ? kKT : 0) + lane, total_tok - 1));
+  const bool resolver = (half ? wave >= 4 : wave < 2) && nseg > 0;
+  const int p_first = (half && wave >= 6 ? kKT : 0) + lane;  // this lane's row in the wave's first tile
+  if (resolver) cursor_init(cursor, seg_start, seg_cum, nseg, min(p_first, total_tok - 1));
+  // IDX: the token index of this lane's row in the next tile the wave resolves, loaded one call
+  // ahead so that the global load's latency is off the resolving wave's path
+  int pend = 0;
+  if constexpr (IDX) {
+    if (resolver && p_first < total_tok) pend = kix[cursor_row(cursor, seg_start, seg_cum, p_first)];
+  }
   const int crow = (wave & 1) ? crow_v : crow_k;  // the resolving waves: even for K, odd for V
-  auto resolve = [&](int32_t* tab, int t) __attribute__((always_inline)) {
+  // Table of tile t; the wave's next table is tile t + step (full items 1, half items 2).
+  auto resolve = [&](int32_t* tab, int t, int step) __attribute__((always_inline)) {
     const int p = t * kKT + lane;
     if (p < total_tok) {
-      const int pos = cursor_row(cursor, seg_start, seg_cum, p);
-      tab[lane] = IDX ? kix[pos] : pos;
+      if constexpr (IDX)
+        tab[lane] = pend;
+      else
+        tab[lane] = cursor_row(cursor, seg_start, seg_cum, p);
     }
     else if (EAR && p < total)
       tab[lane] = crow + cent_idx[p - total_tok];
     else
       tab[lane] = last_row;
+    if constexpr (IDX) {
+      const int pn = p + step * kKT;
+      if (pn < total_tok) pend = kix[cursor_row(cursor, seg_start, seg_cum, pn)];
+    }
   };
   // DMA mapping (group B): wave 4+w, group j moves tile rows 4(kDmaIt w + j) + lane/16.
   const int prow = lane / 16, pch = lane % 16;
@@ -613,12 +632,12 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     // S(0) everywhere, V(0) in group A; tables K(2), K(3), V(2); group B reads the rows of its first
     // copies (K(2), V(1)).
     if (wave == 0) {
-      resolve(rowtab[0][0][0], 0);
-      resolve(rowtab[0][0][1], 1);
+      resolve(rowtab[0][0][0], 0, 1);
+      resolve(rowtab[0][0][1], 1, 1);
     }
     if (wave == 1) {
-      resolve(rowtab[0][1][0], 0);
-      resolve(rowtab[0][1][1], 1);
+      resolve(rowtab[0][1][0], 0, 1);
+      resolve(rowtab[0][1][1], 1, 1);
     }
     __syncthreads();
     if (group_b) {
@@ -631,10 +650,10 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     if (active) scores(k_s0);
     if (active && !group_b) vphase(0);
     if (wave == 0) {
-      resolve(rowtab[0][0][0], 2);
-      resolve(rowtab[0][0][1], 3);
+      resolve(rowtab[0][0][0], 2, 1);
+      resolve(rowtab[0][0][1], 3, 1);
     }
-    if (wave == 1) resolve(rowtab[0][1][0], 2);
+    if (wave == 1) resolve(rowtab[0][1][0], 2, 1);
     __syncthreads();
     int4 rk = make_int4(0, 0, 0, 0), rv = make_int4(0, 0, 0, 0);
     if (group_b) {
@@ -660,8 +679,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       __syncthreads();
       if (!group_b) {
         if (active && t + 1 < ntiles) vphase(t + 1);
-        if (wave == 0 && t + 4 < ntiles) resolve(rowtab[0][0][t & 1], t + 4);
-        if (wave == 1 && t + 3 < ntiles) resolve(rowtab[0][1][(t + 1) & 1], t + 3);
+        if (wave == 0 && t + 4 < ntiles) resolve(rowtab[0][0][t & 1], t + 4, 1);
+        if (wave == 1 && t + 3 < ntiles) resolve(rowtab[0][1][(t + 1) & 1], t + 3, 1);
       } else {
         if (active) mphase(t, v_s0, k_s1);
         rk = dma_rows(rowtab[0][0][(t + 1) & 1]);
@@ -682,8 +701,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       __syncthreads();
       if (!group_b) {
         if (active && t + 2 < ntiles) vphase(t + 2);
-        if (wave == 0 && t + 5 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 5);
-        if (wave == 1 && t + 4 < ntiles) resolve(rowtab[0][1][t & 1], t + 4);
+        if (wave == 0 && t + 5 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 5, 1);
+        if (wave == 1 && t + 4 < ntiles) resolve(rowtab[0][1][t & 1], t + 4, 1);
       } else {
         if (active) mphase(t + 1, v_s1, k_s0);
         rk = dma_rows(rowtab[0][0][t & 1]);
@@ -702,26 +721,26 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       if (u + 1 < n0) dma(vb, rowtab[0][1][(u + 1) & 1], vdst0);
       if (u + 2 < n1) dma(kb, rowtab[1][0][u & 1], kdst1);
       if (u + 1 < n1) dma(vb, rowtab[1][1][(u + 1) & 1], vdst1);
-      if (wave == 4 && u + 3 < n0) resolve(rowtab[0][0][(u + 1) & 1], 2 * (u + 3));
-      if (wave == 5 && u + 2 < n0) resolve(rowtab[0][1][u & 1], 2 * (u + 2));
-      if (wave == 6 && u + 3 < n1) resolve(rowtab[1][0][(u + 1) & 1], 2 * (u + 3) + 1);
-      if (wave == 7 && u + 2 < n1) resolve(rowtab[1][1][u & 1], 2 * (u + 2) + 1);
+      if (wave == 4 && u + 3 < n0) resolve(rowtab[0][0][(u + 1) & 1], 2 * (u + 3), 2);
+      if (wave == 5 && u + 2 < n0) resolve(rowtab[0][1][u & 1], 2 * (u + 2), 2);
+      if (wave == 6 && u + 3 < n1) resolve(rowtab[1][0][(u + 1) & 1], 2 * (u + 3) + 1, 2);
+      if (wave == 7 && u + 2 < n1) resolve(rowtab[1][1][u & 1], 2 * (u + 2) + 1, 2);
     };
     if (wave == 4) {
-      resolve(rowtab[0][0][0], 0);
-      if (n0 > 1) resolve(rowtab[0][0][1], 2);
+      resolve(rowtab[0][0][0], 0, 2);
+      if (n0 > 1) resolve(rowtab[0][0][1], 2, 2);
     }
     if (wave == 5) {
-      resolve(rowtab[0][1][0], 0);
-      if (n0 > 1) resolve(rowtab[0][1][1], 2);
+      resolve(rowtab[0][1][0], 0, 2);
+      if (n0 > 1) resolve(rowtab[0][1][1], 2, 2);
     }
     if (wave == 6 && n1 > 0) {
-      resolve(rowtab[1][0][0], 1);
-      if (n1 > 1) resolve(rowtab[1][0][1], 3);
+      resolve(rowtab[1][0][0], 1, 2);
+      if (n1 > 1) resolve(rowtab[1][0][1], 3, 2);
     }
     if (wave == 7 && n1 > 0) {
-      resolve(rowtab[1][1][0], 1);
-      if (n1 > 1) resolve(rowtab[1][1][1], 3);
+      resolve(rowtab[1][1][0], 1, 2);
+      if (n1 > 1) resolve(rowtab[1][1][1], 3, 2);
     }
     __syncthreads();
     if (group_b) {
@@ -744,8 +763,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
         scores(k1_s0);
       }
     }
-    if (wave == 4 && n0 > 2) resolve(rowtab[0][0][0], 4);
-    if (wave == 6 && n1 > 2) resolve(rowtab[1][0][0], 5);
+    if (wave == 4 && n0 > 2) resolve(rowtab[0][0][0], 4, 2);
+    if (wave == 6 && n1 > 2) resolve(rowtab[1][0][0], 5, 2);
     __syncthreads();
     //   A: h = 2u -> M(u), h = 2u+1 -> V(u+1) on stream 0;  B: h = 2u -> V(u) + fetch, h = 2u+1 -> M(u)
     //   on stream 1.  Group B runs out of tiles first (n1 <= n0) and then only fetches.

@@ -77,13 +77,14 @@ def test_cluster_sort_bit_exact(gpu, bh, n, k):
     np.testing.assert_array_equal(slab.cpu().numpy(), np.take_along_axis(labels, oidx.astype(np.int64), 1))
 
 
-def test_permute_unpermute_bit_exact(gpu):
+@pytest.mark.parametrize("d", [128, 32, 256])  # rows of 256 B (one step per block), 64 B, 512 B
+def test_permute_unpermute_bit_exact(gpu, d):
     from svoo_amd.permute import (apply_inverse_permutation, apply_inverse_permutation_bshd,
                                   permute_pair_by_indices, permute_tensor_by_labels)
 
-    say("permute 1x3x3001x128")
-    x, xt = rand_bf16((1, 3, 3001, 128), 1, gpu)
-    v, vt = rand_bf16((1, 3, 3001, 128), 2, gpu)
+    say("permute 1x3x3001x", d)
+    x, xt = rand_bf16((1, 3, 3001, d), 1, gpu)
+    v, vt = rand_bf16((1, 3, 3001, d), 2, gpu)
     labels = np.random.default_rng(3).integers(0, 50, size=(3, 3001))
     y, idx = permute_tensor_by_labels(xt, torch.from_numpy(labels).to(gpu), 2)
     oidx, _, _ = O.cluster_sort(labels, 50)
