@@ -234,20 +234,11 @@ def test_vbsa_matches_oracle(gpu, h, qn, kn, s, density, seed):
     assert torch.all(out[0, 0, :a] == 0)
 
 
-@pytest.mark.parametrize("ear,kn", [(False, 24), (True, 24), (True, 2000)])
-def test_vbsa_half_items_match_oracle(gpu, ear, kn):
-    """Query clusters whose last 256-query tile holds at most 128 queries (the kernel splits such a
-    tile's KV stream over its two wave groups and merges the two softmax states), for KV streams of
-    1 to several 64-key tiles.  kn = 2000 with EAR leaves no LDS for the second stream: the same
-    sizes then run as full items."""
-    from svoo_amd.co_clustering import dynamic_block_sparse_fwd
-    from svoo_amd.ear import dynamic_block_sparse_prune_fwd
-
-    say("vbsa half items", "ear" if ear else "sap", kn)
-    h = 2
+def _half_item_case(kn, r, h=2):
+    """Query cluster sizes around the 128 / 256 item boundaries (last tiles of 1 to 128 queries become half
+    items), random key cuts and per-row map densities from one short cluster to all-true."""
     qsz = np.array([1, 31, 32, 33, 100, 128, 129, 255, 256, 257, 300, 384, 385, 640, 700], np.int32)
     s = int(qsz.sum())
-    r = np.random.default_rng(40 + kn)
     qs = np.stack([qsz, qsz[::-1]])[None]
     cuts = np.sort(np.stack([r.choice(np.arange(1, s), size=kn - 1, replace=False) for _ in range(h)]), axis=1)
     ks = np.diff(np.concatenate([np.zeros((h, 1), int), cuts, np.full((h, 1), s)], axis=1), axis=1).astype(np.int32)
@@ -263,6 +254,21 @@ def test_vbsa_half_items_match_oracle(gpu, ear, kn):
             else:
                 m[0, b, i] = r.random(kn) < (0.05, 0.15, 0.4, 1.0)[mode - 1]
                 m[0, b, i, small] = True
+    return h, s, qs, ks, m
+
+
+@pytest.mark.parametrize("ear,kn", [(False, 24), (True, 24), (True, 2000)])
+def test_vbsa_half_items_match_oracle(gpu, ear, kn):
+    """Query clusters whose last 256-query tile holds at most 128 queries (the kernel splits such a
+    tile's KV stream over its two wave groups and merges the two softmax states), for KV streams of
+    1 to several 64-key tiles.  kn = 2000 with EAR leaves no LDS for the second stream: the same
+    sizes then run as full items."""
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd
+    from svoo_amd.ear import dynamic_block_sparse_prune_fwd
+
+    say("vbsa half items", "ear" if ear else "sap", kn)
+    r = np.random.default_rng(40 + kn)
+    h, s, qs, ks, m = _half_item_case(kn, r)
     q, qt = rand_bf16((1, h, s, 128), 41, gpu, 0.5)
     k, kt = rand_bf16((1, h, s, 128), 42, gpu, 0.5)
     v, vt = rand_bf16((1, h, s, 128), 43, gpu)
@@ -394,4 +400,28 @@ def test_fused_attention_equals_separate_passes(gpu, h, qn, kn, s, density, seed
     kp, vp = permute_pair_by_indices(k, v, ki)
     ref = apply_inverse_permutation_bshd(dynamic_block_sparse_fwd(qp, kp, vp, m, qst, kst), qi)
     assert out.shape == (1, s, h * 128)
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("kn", [24, 700])
+def test_fused_half_items_equal_separate_passes(gpu, kn):
+    """The fused kernel on half items (each wave group resolving every other table, its index loads one
+    table ahead) gives the same bits as permute + attention + inverse permutation."""
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd, dynamic_block_sparse_fwd_fused
+    from svoo_amd.permute import apply_inverse_permutation_bshd, permute_pair_by_indices
+    from svoo_amd.processor import _permute_rows
+
+    say("fused vbsa half items", kn)
+    r = np.random.default_rng(70 + kn)
+    h, s, qs, ks, m = _half_item_case(kn, r)
+    qi = torch.from_numpy(np.stack([r.permutation(s) for _ in range(h)]).astype(np.int32)).to(gpu)
+    ki = torch.from_numpy(np.stack([r.permutation(s) for _ in range(h)]).astype(np.int32)).to(gpu)
+    _, q = rand_bf16((1, h, s, 128), 71, gpu, 0.5)
+    _, k = rand_bf16((1, h, s, 128), 72, gpu, 0.5)
+    _, v = rand_bf16((1, h, s, 128), 73, gpu)
+    mt, qst, kst = torch.from_numpy(m).to(gpu), torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu)
+    out = dynamic_block_sparse_fwd_fused(q, k, v, mt, qst, kst, qi, ki)
+    qp = _permute_rows(q, qi)
+    kp, vp = permute_pair_by_indices(k, v, ki)
+    ref = apply_inverse_permutation_bshd(dynamic_block_sparse_fwd(qp, kp, vp, mt, qst, kst), qi)
     assert torch.equal(out, ref)
