@@ -469,7 +469,7 @@ extern "C" int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, co
 
 // Workspace layout of svoo_co_cluster (each region 256-byte aligned):
 //   e_hi, e_lo   [bh][jpad_max][128] bf16
-//   counts       [bh][kmax][nchunks] int32   (cluster-sort scratch)
+//   counts       [bh][nchunks][kmax] int32   (cluster-sort scratch)
 //   sums_k       [bh][kc][128] fp64          (key-centroid sums, kept across iterations)
 //   sorted_lab   [bh][n] int32
 //   sums_q       [bh][qc][128] fp64          (query-centroid sums)

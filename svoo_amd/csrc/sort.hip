@@ -1,10 +1,11 @@
 // Stable counting sort of cluster labels (per batch-head row).
 //
 // Three HBM-light passes over labels[BH][N] (int32):
-//   1. hist:    per 1024-token chunk, an LDS histogram -> counts[b][k][chunk]   (cluster-major)
+//   1. hist:    per 1024-token chunk, an LDS histogram -> counts[b][chunk][k]   (chunk-major, so the
+//               write of a chunk's histogram and the scatter's read of its bases are contiguous)
 //   2. scan:    per row, exclusive scan of counts in (cluster, chunk) order      -> chunk bases,
-//               sizes[b][k] and offsets[b][k]; 16 waves each scan a contiguous span 64 entries
-//               at a time (coalesced), after a first pass that sums each span
+//               sizes[b][k] and offsets[b][k]; one thread per cluster sums its chunks, a block
+//               scan gives the cluster offsets, and the thread walks its chunks again
 //   3. scatter: one wave per chunk walks its tokens in order, 64 at a time; the lanes holding the
 //               same label are found with one ballot per label bit (ceil(log2 K) ballots), and
 //               ranked by lane order (popcount of the lower lanes), so equal labels keep their
@@ -36,7 +37,7 @@ __global__ void __launch_bounds__(256) sort_hist_kernel(const int32_t* __restric
   if (bad && err) atomicOr(err, 1);
   __syncthreads();
   int32_t* out = counts + (size_t)b * k * nchunks;
-  for (int i = threadIdx.x; i < k; i += blockDim.x) out[(size_t)i * nchunks + c] = hist[i];
+  for (int i = threadIdx.x; i < k; i += blockDim.x) out[(size_t)c * k + i] = hist[i];  // [chunk][cluster]
 }
 
 constexpr int kScanWaves = 16;
@@ -50,45 +51,46 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
   return v;
 }
 
+// counts [chunk][cluster] -> bases (in place): base of (chunk c, cluster i) = offset of cluster i + the counts of
+// cluster i in chunks before c, which is the stable order (cluster, then token).  One thread per cluster, 1024
+// clusters per pass; every access of a chunk row is contiguous over the threads.
 __global__ void __launch_bounds__(kScanWaves * kWave) sort_scan_kernel(int32_t* __restrict__ counts, int k,
                                                                        int nchunks, int32_t* __restrict__ sizes,
                                                                        int32_t* __restrict__ offsets) {
   __shared__ int wsum[kScanWaves];
-  __shared__ int wbase[kScanWaves + 1];
-  const int b = blockIdx.x, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int b = blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   int32_t* cnt = counts + (size_t)b * k * nchunks;
-  const int total = k * nchunks;
-  const int per = ((total + kScanWaves - 1) / kScanWaves + kWave - 1) / kWave * kWave;
-  const int s0 = min(total, wave * per), s1 = min(total, s0 + per);
-  int acc = 0;
-  for (int i = s0 + lane; i < s1; i += kWave) acc += cnt[i];
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-  if (lane == 0) wsum[wave] = acc;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int r = 0;
-    for (int w = 0; w < kScanWaves; ++w) {
-      wbase[w] = r;
-      r += wsum[w];
+  int carry = 0;  // clusters of the earlier passes
+  for (int i0 = 0; i0 < k; i0 += kScanWaves * kWave) {
+    const int i = i0 + tid;
+    int tot = 0;
+    if (i < k) {
+#pragma unroll 8
+      for (int c = 0; c < nchunks; ++c) tot += cnt[(size_t)c * k + i];
     }
-    wbase[kScanWaves] = r;
-  }
-  __syncthreads();
-  int run = wbase[wave];
-  for (int g = s0; g < s1; g += kWave) {
-    const int i = g + lane;
-    const int v = i < s1 ? cnt[i] : 0;
-    const int inc = wave_inclusive_scan(v, lane);
-    if (i < s1) cnt[i] = run + inc - v;
-    run += __shfl(inc, kWave - 1);
-  }
-  __syncthreads();
-  const int all = wbase[kScanWaves];
-  for (int i = threadIdx.x; i < k; i += kScanWaves * kWave) {
-    const int32_t start = cnt[(size_t)i * nchunks];
-    const int32_t next = (i + 1 < k) ? cnt[(size_t)(i + 1) * nchunks] : all;
-    offsets[(size_t)b * k + i] = start;
-    sizes[(size_t)b * k + i] = next - start;
+    const int inc = wave_inclusive_scan(tot, lane);
+    if (lane == kWave - 1) wsum[wave] = inc;
+    __syncthreads();
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kScanWaves; ++w) {
+      before += w < wave ? wsum[w] : 0;
+      all += wsum[w];
+    }
+    if (i < k) {
+      const int start = carry + before + inc - tot;
+      offsets[(size_t)b * k + i] = start;
+      sizes[(size_t)b * k + i] = tot;
+      int run = start;
+#pragma unroll 8
+      for (int c = 0; c < nchunks; ++c) {
+        const int v = cnt[(size_t)c * k + i];
+        cnt[(size_t)c * k + i] = run;
+        run += v;
+      }
+    }
+    carry += all;
+    __syncthreads();  // wsum is rewritten by the next pass
   }
 }
 
@@ -99,7 +101,7 @@ __global__ void __launch_bounds__(64) sort_scatter_kernel(const int32_t* __restr
   extern __shared__ int32_t base[];
   const int b = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
   const int32_t* bs = bases + (size_t)b * k * nchunks;
-  for (int i = lane; i < k; i += kWave) base[i] = bs[(size_t)i * nchunks + c];
+  for (int i = lane; i < k; i += kWave) base[i] = bs[(size_t)c * k + i];
   __syncthreads();
   const int32_t* lab = labels + (size_t)b * n;
   int32_t* out = sorted_idx + (size_t)b * n;
