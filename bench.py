@@ -216,17 +216,19 @@ def main():
         permute_ms = stages_ms["permute"] + stages_ms["unpermute"]
         permute_fused = False
     else:
-        # The Wan SAP call reads Q/K/V through the sorted indices inside the attention kernel; the permute
+        # The SAP call (Wan, HunyuanVideo) reads Q/K/V through the sorted indices inside the attention kernel; the permute
         # operators (the reference's separate passes) are timed on their own at the same size.
         from svoo_amd.permute import apply_inverse_permutation_bshd, permute_pair_by_indices
         from svoo_amd.processor import _permute_rows
 
         clu = last["clustering"]
+        # HunyuanVideo: the whole sequence's indices (text rows map to themselves)
+        qix, kix = last.get("q_idx", clu["q_sorted_idx"]), last.get("k_idx", clu["k_sorted_idx"])
 
         def permutes():
-            qp = _permute_rows(q, clu["q_sorted_idx"])
-            permute_pair_by_indices(k, v, clu["k_sorted_idx"])
-            apply_inverse_permutation_bshd(qp, clu["q_sorted_idx"])
+            qp = _permute_rows(q, qix)
+            permute_pair_by_indices(k, v, kix)
+            apply_inverse_permutation_bshd(qp, qix)
 
         permutes()
         torch.cuda.synchronize()

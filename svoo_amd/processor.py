@@ -595,7 +595,9 @@ class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
         return dyn_map, qc_sz, kc_sz, _extend_with_text(q_sorted_indices, video_length, context_length)
 
     def attention_core_logic(self, query, key, value, timestep, layer_idx=None, cu_max_seqlens=None):
-        """Hunyuan SVOO attention for ``[1, H, S, D]`` Q/K/V (``:1031-1110``); returns ``[1, H, S, D]``."""
+        """Hunyuan SVOO attention for ``[1, H, S, D]`` Q/K/V (``:1031-1110``); returns ``[1, H, S, D]``
+        (with ``fuse_permutes``, the transposed view of a ``[1, S, H, D]`` buffer: same values, and the
+        caller's ``transpose(1, 2).flatten(2, 3)`` becomes a view)."""
         cfg, num_heads, seq_len, dim = query.size()
         assert cfg == 1, "Batch size must be 1 for kmeans block sparse attention"
         prompt_length, context_length = self.prompt_length, self.context_length
@@ -640,6 +642,16 @@ class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
         dyn_map, qc_sz, kc_sz, q_idx = self.dynamic_map_post_processing(
             dyn_map, q_sizes, k_sizes, r["q_sorted_idx"], video_length, context_length, prompt_length, unprompt_length)
         k_idx = _extend_with_text(r["k_sorted_idx"], video_length, context_length)
+        if self.fuse_permutes:
+            # One kernel on token-order Q/K/V through q_idx / k_idx (text rows map to themselves); it writes
+            # [1, S, H*D] in token order, returned as its [1, H, S, D] transposed view (the same values as the
+            # separate passes; the caller's transpose(1, 2).flatten(2, 3) is then a view, not a copy).
+            self._last_call = dict(clustering=r, map=dyn_map, lengths=lengths, min_kc_ratio=min_kc_ratio,
+                                   q_sizes=qc_sz, k_sizes=kc_sz, q_idx=q_idx, k_idx=k_idx)
+            out = dynamic_block_sparse_fwd_fused(query.contiguous(), key.contiguous(), value.contiguous(), dyn_map,
+                                                 qc_sz, kc_sz, q_idx, k_idx, validate=False)
+            self._mark("attention")
+            return out.view(cfg, seq_len, num_heads, dim).transpose(1, 2)
         q_perm = _permute_rows(query.contiguous(), q_idx)
         k_perm, v_perm = permute_pair_by_indices(key.contiguous(), value.contiguous(), k_idx)
         self._mark("permute")
