@@ -135,7 +135,7 @@ int svoo_weighted_softmax(const uint16_t* scores, const float* weights, long lon
  *   For each (b, i): O_i = softmax(Q_i K_S^T / sqrt(D)) V_S over the active key clusters S (ascending),
  *   fp32 online softmax, bf16 MFMA; rows of a query cluster with no active keys are zero.
  *   status (device int32, may be NULL) receives 0, or 1 when the sizes of a head do not sum to S
- *   (that head's output is then left unwritten).
+ *   (every output row of that head is then NaN, so the error is visible without a host read-back).
  *   Limits (SVOO_ERR_UNSUPPORTED beyond them): D = 128, KN <= 4096, ceil(S / 256) + QN < 32768.
  * Replaces dynamic_block_sparse_fwd_flashinfer (svoo/co_clustering.py:1231-1311, with the plan of
  * svoo/utils/flashinfer_sparse.py:43-244) and dynamic_block_sparse_fwd_triton (svoo/co_clustering.py:949-1228).

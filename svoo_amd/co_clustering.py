@@ -342,6 +342,17 @@ def identify_dynamic_map(query_centroids, key_centroids, q_cluster_sizes, k_clus
 # ------------------------------------------------------------------------------------------------
 # Variable-block-sparse attention
 # ------------------------------------------------------------------------------------------------
+def _check_host_sizes(sizes, s: int, name: str) -> None:
+    """Sizes that live on the host (the reference's ``is_cpu=True`` case) are checked before they are
+    copied, at no cost to the GPU stream (``svoo/co_clustering.py:1138-1139``).  Device sizes are
+    checked by the plan kernel: the rows of a head whose sizes do not sum to ``S`` come back NaN."""
+    if isinstance(sizes, torch.Tensor) and sizes.is_cuda:
+        return
+    tot = torch.as_tensor(sizes).to(torch.int64)
+    if tot.dim() == 0 or bool((tot < 0).any()) or not bool((tot.sum(-1) == s).all()):
+        raise AssertionError(f"{name}: cluster sizes of every head must sum to S={s}")
+
+
 def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate: bool = True):
     """Variable-block-sparse attention over cluster-contiguous tokens.
 
@@ -349,7 +360,9 @@ def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate
     ``kc_size [B, H, Kc]``.  Query cluster ``i`` attends to the concatenation of its active key
     clusters with ``scale = D ** -0.5``; clusters without active keys produce zeros.  With
     ``validate`` the sizes of every head must sum to ``S`` (checked on the host after the call, as
-    the reference asserts, ``svoo/co_clustering.py:1138-1139``).
+    the reference asserts, ``svoo/co_clustering.py:1138-1139``).  Sizes passed as host tensors are
+    checked before the launch in either case; without ``validate`` a head whose device sizes are
+    inconsistent comes back as NaN rows (no host read-back).
     """
     assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
     assert q.dtype == k.dtype == v.dtype, "Input dtypes must match"
@@ -360,6 +373,8 @@ def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate
     qn = qc_size.shape[-1]
     kn = kc_size.shape[-1]
     assert dynamic_map.shape == (b, h, qn, kn), "dynamic_map must be [B, H, Qc, Kc]"
+    _check_host_sizes(qc_size, s, "qc_size")
+    _check_host_sizes(kc_size, s, "kc_size")
     dev = q.device
     bh = b * h
     qq = q.reshape(bh, s, d).contiguous()
@@ -397,6 +412,8 @@ def dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, qc_size, kc_s
     qn = qc_size.shape[-1]
     kn = kc_size.shape[-1]
     assert dynamic_map.shape == (b, h, qn, kn), "dynamic_map must be [B, H, Qc, Kc]"
+    _check_host_sizes(qc_size, s, "qc_size")
+    _check_host_sizes(kc_size, s, "kc_size")
     dev = query.device
     bh = b * h
     qq, kk, vv = (t.reshape(bh, s, d).contiguous() for t in (query, key, value))
@@ -421,7 +438,8 @@ def dynamic_block_sparse_fwd_flashinfer(q, k, v, block_mask_map, block_row_sz, b
     """Drop-in for ``dynamic_block_sparse_fwd_flashinfer`` (``svoo/co_clustering.py:1231-1311``).
 
     The plan is built on the device, so ``is_cpu`` only states where the map and sizes live; they
-    are moved to the GPU if needed.  No 128 MiB workspace and no host round trip per call.
+    are moved to the GPU if needed.  No 128 MiB workspace and no host round trip per call.  Host-side
+    sizes are checked before the copy; inconsistent device sizes give NaN rows for that head.
     """
     return dynamic_block_sparse_fwd(q, k, v, block_mask_map, block_row_sz, block_col_sz, validate=False)
 

@@ -110,7 +110,8 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
     }
     if (tid == 0) {
       qo[qn] = (int32_t)(tot & 0xffffffffll);
-      nitems[b] = ok ? (int32_t)(tot >> 32) : 0;
+      // -1 marks a head whose sizes do not sum to S: the attention fills its rows with NaN
+      nitems[b] = ok ? (int32_t)(tot >> 32) : -1;
       if (!ok && status) atomicOr(status, 1);
     }
   }
@@ -307,7 +308,25 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   const long long item = xcd_item(blockIdx.x);
   if (item >= total_items) return;
   const int b = order[(int)(item / cap)], local = (int)(item % cap);
-  if (local >= nitems[b]) return;
+  const int head_items = nitems[b];
+  if (local >= head_items) {
+    if (head_items < 0 && (long long)local * kQTile < s) {
+      // Sizes of this head do not sum to S (the reference asserts, svoo/co_clustering.py:1138-1139):
+      // item slot `local` writes NaN over token rows [local * kQTile, +kQTile) of the head, so the
+      // failure is visible in the output instead of leaving the buffer's old contents.  cap >=
+      // ceil(S / kQTile), so the slots cover every row.  Rows are addressed by token (not through
+      // the sorted indices, which may be as inconsistent as the sizes).
+      const int r0 = local * kQTile, r1 = min(s, r0 + kQTile);
+      const u32x4_t nan4 = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+      for (int idx = threadIdx.x; idx < (r1 - r0) * 16; idx += kVWaves * kWave) {
+        const int t = r0 + idx / 16;
+        uint16_t* row = IDX ? o + (((size_t)(b / heads) * s + t) * heads + (b % heads)) * 128
+                            : o + ((size_t)b * s + t) * 128;
+        ((u32x4_t*)row)[idx % 16] = nan4;
+      }
+    }
+    return;
+  }
   const int packed = items[(size_t)b * cap + local];
   const int ci = packed >> 16, tile = packed & 0x7fff;
   const bool half = HC && (packed & 0x8000) != 0;

@@ -22,7 +22,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from .co_clustering import _bf16_value, _ratio_values
+from .co_clustering import _bf16_value, _check_host_sizes, _ratio_values
 
 __all__ = [
     "ear_row_params",
@@ -241,7 +241,8 @@ def dynamic_block_sparse_prune_fwd(q, k, v, k_centroids, v_centroids, block_mask
 
     Query cluster ``i`` attends, in one softmax, to the tokens of its active key clusters and to the
     centroid pairs ``(Kc_j, Vc_j)`` of its inactive ones with logit ``q . Kc_j / sqrt(D) +
-    log(|K_j| + 1e-6)``.  With ``validate`` the sizes of every head must sum to ``S``."""
+    log(|K_j| + 1e-6)``.  With ``validate`` the sizes of every head must sum to ``S``; host-side sizes
+    are checked before the launch, and without ``validate`` inconsistent device sizes give NaN rows."""
     assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
     if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
         raise TypeError("dynamic_block_sparse_prune_fwd: the MI355X path computes in bfloat16")
@@ -251,6 +252,8 @@ def dynamic_block_sparse_prune_fwd(q, k, v, k_centroids, v_centroids, block_mask
     assert k.shape == q.shape and v.shape == q.shape, "q, k, v must share one shape"
     assert block_mask_map.shape == (b, h, qn, kn)
     assert k_centroids.shape == (b, h, kn, d) and v_centroids.shape == (b, h, kn, d)
+    _check_host_sizes(block_row_sz, s, "block_row_sz")
+    _check_host_sizes(block_col_sz, s, "block_col_sz")
     dev = q.device
     bh = b * h
     qq, kk, vv = (t.reshape(bh, s, d).contiguous() for t in (q, k, v))

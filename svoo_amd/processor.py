@@ -595,12 +595,24 @@ class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
         return dyn_map, qc_sz, kc_sz, _extend_with_text(q_sorted_indices, video_length, context_length)
 
     def attention_core_logic(self, query, key, value, timestep, layer_idx=None, cu_max_seqlens=None):
-        """Hunyuan SVOO attention for ``[1, H, S, D]`` Q/K/V (``:1031-1110``); returns ``[1, H, S, D]``
-        (with ``fuse_permutes``, the transposed view of a ``[1, S, H, D]`` buffer: same values, and the
-        caller's ``transpose(1, 2).flatten(2, 3)`` becomes a view)."""
+        """Hunyuan SVOO attention for ``[1, H, S, D]`` Q/K/V (``:1031-1110``); returns ``[1, H, S, D]``.
+
+        Layout: with ``fuse_permutes`` (the default) the result is the ``transpose(1, 2)`` view of a
+        contiguous ``[1, S, H, D]`` buffer, so the caller's ``transpose(1, 2).flatten(2, 3)`` is free;
+        it is not contiguous, so a caller that needs ``.view`` on it calls ``.contiguous()`` first (the
+        reference returns a contiguous ``[1, H, S, D]``).  With ``fuse_permutes = False`` it is
+        contiguous.  The values are identical either way.
+
+        ``_last_call`` holds the post-processed ``map``, ``q_sizes`` and ``k_sizes`` (``Qc + 2`` /
+        ``Kc + 2`` clusters, text last) and ``video_lengths``, the kept key clusters per row of the
+        video-only map before the text clusters are added."""
         cfg, num_heads, seq_len, dim = query.size()
         assert cfg == 1, "Batch size must be 1 for kmeans block sparse attention"
-        prompt_length, context_length = self.prompt_length, self.context_length
+        prompt_length, context_length = int(self.prompt_length), int(self.context_length)
+        if not 0 <= prompt_length <= context_length:
+            # A prompt longer than the text context would make the padding cluster's size negative and
+            # every head's plan invalid.
+            raise ValueError(f"prompt_length={prompt_length} must lie in [0, context_length={context_length}]")
         video_length = self.num_frame * self.frame_size
         assert seq_len == context_length + video_length, (
             f"Query Shape: {seq_len} is not equivalent to {context_length} + {self.num_frame} * {self.frame_size}"
@@ -646,7 +658,7 @@ class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
             # One kernel on token-order Q/K/V through q_idx / k_idx (text rows map to themselves); it writes
             # [1, S, H*D] in token order, returned as its [1, H, S, D] transposed view (the same values as the
             # separate passes; the caller's transpose(1, 2).flatten(2, 3) is then a view, not a copy).
-            self._last_call = dict(clustering=r, map=dyn_map, lengths=lengths, min_kc_ratio=min_kc_ratio,
+            self._last_call = dict(clustering=r, map=dyn_map, video_lengths=lengths, min_kc_ratio=min_kc_ratio,
                                    q_sizes=qc_sz, k_sizes=kc_sz, q_idx=q_idx, k_idx=k_idx)
             out = dynamic_block_sparse_fwd_fused(query.contiguous(), key.contiguous(), value.contiguous(), dyn_map,
                                                  qc_sz, kc_sz, q_idx, k_idx, validate=False)
@@ -655,8 +667,8 @@ class Hunyuan_SAPAttn_Processor(WanAttn_SAPAttn_Processor):
         q_perm = _permute_rows(query.contiguous(), q_idx)
         k_perm, v_perm = permute_pair_by_indices(key.contiguous(), value.contiguous(), k_idx)
         self._mark("permute")
-        self._last_call = dict(clustering=r, map=dyn_map, lengths=lengths, min_kc_ratio=min_kc_ratio,
-                               q_sizes=qc_sz, k_sizes=kc_sz)
+        self._last_call = dict(clustering=r, map=dyn_map, video_lengths=lengths, min_kc_ratio=min_kc_ratio,
+                               q_sizes=qc_sz, k_sizes=kc_sz, q_idx=q_idx, k_idx=k_idx)
         out_perm = dynamic_block_sparse_fwd(q_perm, k_perm, v_perm, dyn_map, qc_sz, kc_sz, validate=False)
         self._mark("attention")
         if self.enable_mem_save:

@@ -308,6 +308,35 @@ def test_vbsa_rejects_inconsistent_sizes(gpu):
     m = torch.ones(1, 1, 2, 2, dtype=torch.bool, device=gpu)
     with pytest.raises(AssertionError):
         dynamic_block_sparse_fwd_triton(qt, qt, qt, m, qs, qs)
+    with pytest.raises(AssertionError):  # sizes on the host are checked before any launch
+        dynamic_block_sparse_fwd_triton(qt, qt, qt, m, qs.cpu(), qs)
+
+
+def test_vbsa_fills_heads_with_inconsistent_sizes_with_nan(gpu):
+    """Without the host check (the processors' path: no read-back), a head whose sizes do not sum to S
+    comes back as NaN in every row, on the separate and the fused kernel; the other heads are computed."""
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd, dynamic_block_sparse_fwd_fused
+
+    say("vbsa bad sizes in one of two heads -> NaN rows")
+    s = 300
+    q, qt = rand_bf16((1, 2, s, 128), 11, gpu)
+    k, kt = rand_bf16((1, 2, s, 128), 12, gpu)
+    v, vt = rand_bf16((1, 2, s, 128), 13, gpu)
+    qs = np.array([[[100, 200], [100, 200]]], np.int32)
+    ks = np.array([[[150, 150], [150, 140]]], np.int32)  # head 1: 290 != 300
+    m = np.ones((1, 2, 2, 2), bool)
+    qst, kst, mt = torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu), torch.from_numpy(m).to(gpu)
+    out = dynamic_block_sparse_fwd(qt, kt, vt, mt, qst, kst, validate=False)
+    torch.cuda.synchronize()
+    assert torch.isnan(out[0, 1]).all()
+    assert not torch.isnan(out[0, 0]).any()
+    _attn_check(out[:, :1], O.block_sparse_attention(q[:, :1], k[:, :1], v[:, :1], m[:, :1], qs[:, :1], ks[:, :1]))
+    ident = torch.arange(s, dtype=torch.int32, device=gpu).expand(2, s).contiguous()
+    fused = dynamic_block_sparse_fwd_fused(qt, kt, vt, mt, qst, kst, ident, ident, validate=False)
+    torch.cuda.synchronize()
+    fo = fused.view(s, 2, 128)
+    assert torch.isnan(fo[:, 1]).all()
+    assert torch.equal(fo[:, 0], out[0, 0])
 
 
 def test_vbsa_segments_expand_to_reference_plan(gpu):
