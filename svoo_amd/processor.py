@@ -30,7 +30,8 @@ import torch.nn.functional as F
 from .co_clustering import (block_mask_lengths, co_cluster_tokens_full, dynamic_block_sparse_fwd,
                             dynamic_block_sparse_fwd_fused)
 from .ear import dynamic_block_sparse_prune_fwd, ear_map_and_value_centroids
-from .sparsity.exact import compute_exact_attention_sparsity, format_sparsity_log, has_completed_sparsity_entry
+from .sparsity.exact import (compute_exact_attention_sparsity, format_sparsity_log, has_completed_sparsity_entry,
+                             record_sparsity_entry)
 from .permute import apply_inverse_permutation, apply_inverse_permutation_bshd, permute_pair_by_indices
 from . import _lib
 
@@ -255,6 +256,7 @@ class WanAttn_SAPAttn_Processor:
                 os.makedirs(d, exist_ok=True)
             with open(out, "a") as f:
                 f.write("\n".join(lines) + "\n")
+            record_sparsity_entry(out, self.layer_idx, step, range(len(per_head)))
 
     def flash_attention(self, query, key, value):
         """Dense attention of the full-precision gate (``svoo/models/wan/attention.py:329-331``)."""

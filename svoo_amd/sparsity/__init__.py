@@ -8,6 +8,7 @@ from .exact import (
     exact_counts_from_scores,
     format_sparsity_log,
     has_completed_sparsity_entry,
+    record_sparsity_entry,
 )
 from .merge import merge_sparsity_data, parse_sparsity_file, save_to_csv
 
@@ -18,6 +19,7 @@ __all__ = [
     "exact_counts_from_scores",
     "format_sparsity_log",
     "has_completed_sparsity_entry",
+    "record_sparsity_entry",
     "merge_sparsity_data",
     "parse_sparsity_file",
     "save_to_csv",

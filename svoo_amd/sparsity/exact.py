@@ -19,38 +19,50 @@ from __future__ import annotations
 
 import os
 import re
-from typing import List, Tuple
+from typing import Dict, List, Set, Tuple
 
 import torch
 
 from .. import _lib
 
 DEFAULT_SPARSITY_THRESHOLD = 0.95
+# Share of the device's free memory one query chunk's bf16 scores may take when the chunk is sized
+# automatically; SVOO_SPARSITY_AUTO_MEM_FRACTION overrides it (the reference's knob, same meaning).
 DEFAULT_AUTO_MEMORY_FRACTION = 0.45
-# bf16 scores plus the GEMM's own workspace, per score (the counts need no per-score scratch)
-_BYTES_PER_SCORE = 4
+# Above this many score bytes per chunk the count kernel, not the GEMM launch count, sets the time,
+# so larger chunks buy nothing and only hold memory.
+_MAX_CHUNK_SCORE_BYTES = 4 << 30
+_SCORE_BYTES = 2  # bf16 scores; the counts need no per-score scratch
 _SPARSITY_HEADER_RE = re.compile(r"\[Sparsity\] Layer (\d+) \| Type: \w+ \| Step: (\d+)")
 _SPARSITY_HEAD_RE = re.compile(r"\s*Head\s+(\d+):\s+Sparsity=")
 
 
-def _auto_query_chunk_size(query: torch.Tensor, key: torch.Tensor) -> int:
-    """Largest query chunk whose bf16 scores fit a fraction of free device memory (``exact.py:21-47``)."""
-    batch, num_heads, seq_len_q, _ = query.size()
-    seq_len_k = key.size(2)
+def _memory_share() -> float:
+    """The free-memory share from the environment, or the default when unset or not a number in (0, 1)."""
+    raw = os.environ.get("SVOO_SPARSITY_AUTO_MEM_FRACTION")
     try:
-        free_bytes, _ = torch.cuda.mem_get_info(query.device)
-    except Exception:
-        return min(128, seq_len_q)
-    try:
-        frac = float(os.environ.get("SVOO_SPARSITY_AUTO_MEM_FRACTION", DEFAULT_AUTO_MEMORY_FRACTION))
+        share = float(raw) if raw is not None else DEFAULT_AUTO_MEMORY_FRACTION
     except ValueError:
-        frac = DEFAULT_AUTO_MEMORY_FRACTION
-    frac = min(0.90, max(0.05, frac))
-    per_query = max(1, batch * num_heads * seq_len_k * _BYTES_PER_SCORE)
-    chunk = int(free_bytes * frac / per_query)
-    if chunk >= 16:
-        chunk = (chunk // 8) * 8
-    return max(1, min(seq_len_q, chunk))
+        return DEFAULT_AUTO_MEMORY_FRACTION
+    return share if 0.0 < share < 1.0 else DEFAULT_AUTO_MEMORY_FRACTION
+
+
+def _query_chunk_rows(query: torch.Tensor, key: torch.Tensor) -> int:
+    """Query rows per chunk when the caller leaves it to us (``svoo/sparsity/exact.py:19-42`` sizes the
+    reference's fp32 sort workspace the same way).
+
+    One chunk of ``r`` rows holds ``B * H * r * S_k`` bf16 scores.  The budget is the smaller of
+    ``_MAX_CHUNK_SCORE_BYTES`` and a share of free device memory; rows come in multiples of 64 (whole
+    MFMA tiles of the score GEMM) once the budget allows 64.
+    """
+    b, h, rows_q, _ = query.shape
+    bytes_per_row = max(1, b * h * key.size(2) * _SCORE_BYTES)
+    free = torch.cuda.mem_get_info(query.device)[0]
+    budget = min(_MAX_CHUNK_SCORE_BYTES, int(free * _memory_share()))
+    rows = budget // bytes_per_row
+    if rows >= 64:
+        rows -= rows % 64
+    return int(min(rows_q, max(1, rows)))
 
 
 def _sample_query_rows(query: torch.Tensor, sample_size: int):
@@ -106,18 +118,29 @@ def compute_exact_attention_sparsity(
         raise ValueError("compute_exact_attention_sparsity runs on a HIP device")
     query, sampled = _sample_query_rows(query, query_sample_size)
     rows_q = query.size(2)
-    if batch_size is None or batch_size <= 0:
-        batch_size = _auto_query_chunk_size(query, key)
-    else:
-        batch_size = min(int(batch_size), rows_q)
+    auto = batch_size is None or batch_size <= 0
+    chunk = _query_chunk_rows(query, key) if auto else min(int(batch_size), rows_q)
     scale = dim ** -0.5
     key_t = key.transpose(-2, -1)
     parts = []
-    for q0 in range(0, rows_q, batch_size):
-        qb = query[:, :, q0:q0 + batch_size, :]
-        scores = torch.matmul(qb, key_t)  # bf16 [B, H, c, Sk]
-        parts.append(exact_counts_from_scores(scores, scale, threshold))
+    q0 = 0
+    while q0 < rows_q:
+        try:
+            scores = torch.matmul(query[:, :, q0:q0 + chunk, :], key_t)  # bf16 [B, H, c, Sk]
+            part = exact_counts_from_scores(scores, scale, threshold)
+        except torch.cuda.OutOfMemoryError:
+            # Free memory can shrink between the sizing and the GEMM (other streams, the caching
+            # allocator's fragmentation): an automatic chunk halves and the same rows are retried
+            # (svoo/sparsity/exact.py:218-230).  An explicit chunk size is the caller's to fix.
+            if not auto or chunk == 1:
+                raise
+            scores = None
+            torch.cuda.empty_cache()
+            chunk = max(1, chunk // 2)
+            continue
         del scores
+        parts.append(part)
+        q0 += chunk
     counts = torch.cat(parts, dim=2)
     per_query = counts.double() / float(seq_len_k)
     per_head = per_query.mean(dim=(0, 2))
@@ -126,46 +149,72 @@ def compute_exact_attention_sparsity(
         "attn_scores_shape": [batch, num_heads, sampled, seq_len_k],
         "seq_len": seq_len_q,
         "sampled_seq_len": sampled,
-        "chunk_size": batch_size,
+        "chunk_size": chunk,
     }
     return avg, per_head.cpu().tolist(), stats
 
 
-_COMPLETION_CACHE: dict = {}
+def _resume_requested() -> bool:
+    """``SVOO_SPARSITY_RESUME`` set to a true value (1, true, yes, on; any case) turns the resume guard on."""
+    return os.environ.get("SVOO_SPARSITY_RESUME", "").strip().lower() in {"1", "true", "yes", "on"}
 
 
-def _resume_enabled() -> bool:
-    return os.environ.get("SVOO_SPARSITY_RESUME", "0") not in ("0", "", "false", "False")
+class SparsityLogIndex:
+    """The (layer, step) -> heads entries of one raw sparsity log.
+
+    The log is parsed once, when the guard first asks about it (a resumed run sees what the interrupted
+    one wrote); afterwards the index learns this process's own appends through :meth:`add`, so a long
+    profiling run never re-reads the growing file.  Entries another process appends to the same file
+    after the first read are not seen.
+    """
+
+    def __init__(self, path: str):
+        self.path = path
+        self.heads: Dict[Tuple[int, int], Set[int]] = {}
+        entry = None
+        try:
+            with open(path, "r", encoding="utf-8") as f:
+                for line in f:
+                    m = _SPARSITY_HEADER_RE.match(line)
+                    if m:
+                        entry = self.heads.setdefault((int(m.group(1)), int(m.group(2))), set())
+                    elif entry is not None:
+                        hm = _SPARSITY_HEAD_RE.match(line)
+                        if hm:
+                            entry.add(int(hm.group(1)))
+        except OSError:
+            pass
+
+    def add(self, layer_idx: int, step: int, heads) -> None:
+        self.heads.setdefault((int(layer_idx), int(step)), set()).update(int(h) for h in heads)
+
+    def complete(self, layer_idx: int, step: int, num_heads: int) -> bool:
+        have = self.heads.get((int(layer_idx), int(step)), ())
+        return all(h in have for h in range(int(num_heads)))
+
+
+_LOG_INDEX: Dict[str, SparsityLogIndex] = {}
+
+
+def _log_index(output_file: str) -> SparsityLogIndex:
+    key = os.path.realpath(output_file)
+    if key not in _LOG_INDEX:
+        _LOG_INDEX[key] = SparsityLogIndex(key)
+    return _LOG_INDEX[key]
 
 
 def has_completed_sparsity_entry(output_file: str, layer_idx: int, step: int, num_heads: int) -> bool:
     """Opt-in resume guard (``SVOO_SPARSITY_RESUME``): True when the raw log already holds every head of
-    this layer/step (``svoo/sparsity/exact.py:58-107``).  The file is read incrementally."""
-    if not _resume_enabled() or not output_file or not os.path.exists(output_file):
+    this layer/step, so the measurement can be skipped (``svoo/sparsity/exact.py:54-102``)."""
+    if not _resume_requested() or not output_file or not os.path.exists(output_file):
         return False
-    try:
-        st = os.stat(output_file)
-        ident = (st.st_dev, st.st_ino)
-        cache = _COMPLETION_CACHE.get(output_file)
-        if cache is None or cache["id"] != ident or st.st_size < cache["offset"]:
-            cache = {"id": ident, "offset": 0, "key": None, "heads": {}}
-            _COMPLETION_CACHE[output_file] = cache
-        with open(output_file, "r", encoding="utf-8") as f:
-            f.seek(cache["offset"])
-            for line in f:
-                m = _SPARSITY_HEADER_RE.match(line)
-                if m:
-                    cache["key"] = (int(m.group(1)), int(m.group(2)))
-                    cache["heads"].setdefault(cache["key"], set())
-                    continue
-                if cache["key"] is not None:
-                    hm = _SPARSITY_HEAD_RE.match(line)
-                    if hm:
-                        cache["heads"][cache["key"]].add(int(hm.group(1)))
-            cache["offset"] = f.tell()
-        return set(range(int(num_heads))) <= cache["heads"].get((int(layer_idx), int(step)), set())
-    except OSError:
-        return False
+    return _log_index(output_file).complete(layer_idx, step, num_heads)
+
+
+def record_sparsity_entry(output_file: str, layer_idx: int, step: int, heads) -> None:
+    """Tell the resume guard about lines this process appended to ``output_file``."""
+    if output_file and os.path.realpath(output_file) in _LOG_INDEX:
+        _log_index(output_file).add(layer_idx, step, heads)
 
 
 def format_sparsity_log(layer_idx: int, attn_type: str, step: int, threshold: float, avg: float,

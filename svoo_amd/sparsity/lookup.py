@@ -13,7 +13,11 @@ from typing import Dict, List, Optional, Tuple
 
 
 class SparsityLookup:
-    """In-memory lookup table for per-step, per-layer, per-head sparsity."""
+    """A profile CSV held as a ``{(step, layer, head): ratio}`` dict, read by the online mask every step.
+
+    The CSV is parsed once at construction; lookups are plain dict reads, so the processors can query
+    it per call without touching the file or the GPU.
+    """
 
     def __init__(self, csv_path: str, verbose: bool = True):
         self.lookup_dict: Dict[Tuple[int, int, int], float] = {}
@@ -24,20 +28,20 @@ class SparsityLookup:
         if not path.exists():
             raise FileNotFoundError(f"Sparsity CSV file not found: {csv_path}")
         with open(path, "r", encoding="utf-8") as f:
-            for row in csv.DictReader(f):
-                key = (int(row["Step"]), int(row["Layer"]), int(row["Head"]))
-                self.lookup_dict[key] = float(row["Sparsity"])
+            self.lookup_dict.update(
+                ((int(r["Step"]), int(r["Layer"]), int(r["Head"])), float(r["Sparsity"])) for r in csv.DictReader(f))
         if verbose:
             print(f"Loaded {len(self.lookup_dict)} sparsity entries from {csv_path}")
 
     def get_sparsity(self, step: int, layer: int, head: int) -> Optional[float]:
-        """One value, or ``None`` when the entry is missing."""
+        """The ratio stored for ``(step, layer, head)``; ``None`` if the profile has no such row."""
         return self.lookup_dict.get((step, layer, head))
 
     def get_sparsity_batch(self, step: int, layer: int, num_heads: int) -> List[float]:
-        """Values of every head of one step/layer; missing (or zero) entries read as ``0.0``."""
+        """Ratios of heads ``0 .. num_heads - 1`` at one step and layer; an absent or zero row gives ``0.0``."""
         return [self.get_sparsity(step, layer, h) or 0.0 for h in range(num_heads)]
 
     def has_data_for_step_layer(self, step: int, layer: int, num_heads: int = 12) -> bool:
-        """True only when every expected head exists for this step/layer."""
+        """Whether the profile covers all ``num_heads`` heads of this step and layer (a partial layer is
+        treated as absent by the processors, which then fall back to the scalar ratio)."""
         return all(self.get_sparsity(step, layer, h) is not None for h in range(num_heads))

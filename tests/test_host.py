@@ -292,19 +292,79 @@ def test_sparsity_log_merge_roundtrip(tmp_path):
 
 
 def test_sparsity_resume_guard(tmp_path, monkeypatch):
-    from svoo_amd.sparsity import format_sparsity_log, has_completed_sparsity_entry
+    from svoo_amd.sparsity import format_sparsity_log, has_completed_sparsity_entry, record_sparsity_entry
 
     log = tmp_path / "raw.txt"
     log.write_text("\n".join(format_sparsity_log(3, "self", 7, 0.95, 0.1, [0.1] * 4, 50, 50)) + "\n")
     monkeypatch.delenv("SVOO_SPARSITY_RESUME", raising=False)
     assert not has_completed_sparsity_entry(str(log), 3, 7, 4)  # opt-in only
-    monkeypatch.setenv("SVOO_SPARSITY_RESUME", "1")
+    for off in ("0", "false", "no", ""):
+        monkeypatch.setenv("SVOO_SPARSITY_RESUME", off)
+        assert not has_completed_sparsity_entry(str(log), 3, 7, 4)
+    monkeypatch.setenv("SVOO_SPARSITY_RESUME", "True")
     assert has_completed_sparsity_entry(str(log), 3, 7, 4)
     assert not has_completed_sparsity_entry(str(log), 3, 7, 5)
     assert not has_completed_sparsity_entry(str(log), 3, 8, 4)
-    with open(log, "a") as f:  # appended entries are picked up incrementally
+    # this process's own appends reach the guard through record_sparsity_entry, without a re-read
+    with open(log, "a") as f:
         f.write("\n".join(format_sparsity_log(3, "self", 8, 0.95, 0.1, [0.1] * 4, 50, 50)) + "\n")
+    record_sparsity_entry(str(log), 3, 8, range(4))
     assert has_completed_sparsity_entry(str(log), 3, 8, 4)
+    # a resumed run (a fresh index) parses the file once, including partial entries
+    from svoo_amd.sparsity import exact
+
+    part = tmp_path / "partial.txt"
+    part.write_text("\n".join(format_sparsity_log(0, "self", 2, 0.95, 0.1, [0.1] * 3, 50, 50)[:3]) + "\n")
+    assert exact.SparsityLogIndex(str(part)).complete(0, 2, 2)
+    assert not exact.SparsityLogIndex(str(part)).complete(0, 2, 3)
+    assert not exact.SparsityLogIndex(str(tmp_path / "absent.txt")).complete(0, 1, 1)
+
+
+def test_sparsity_chunk_rows_and_oom_backoff(monkeypatch):
+    """Automatic query chunks fill a share of free memory in whole 64-row steps, capped at 4 GiB of bf16
+    scores; an out-of-memory error in a chunk halves it and retries the same rows (the counts equal one
+    unchunked pass), while an explicit chunk size re-raises."""
+    from svoo_amd.sparsity import exact
+
+    q = torch.zeros(1, 2, 5000, 128)
+    k = torch.zeros(1, 2, 3000, 128)
+    per_row = 2 * 3000 * 2
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda dev=None: (per_row * 1000, 1 << 40))
+    monkeypatch.delenv("SVOO_SPARSITY_AUTO_MEM_FRACTION", raising=False)
+    assert exact._query_chunk_rows(q, k) == 448  # 0.45 * 1000 rows -> 450 -> 448
+    monkeypatch.setenv("SVOO_SPARSITY_AUTO_MEM_FRACTION", "0.05")
+    assert exact._query_chunk_rows(q, k) == 50  # below 64 rows: no rounding
+    for bad in ("x", "0", "1.5"):
+        monkeypatch.setenv("SVOO_SPARSITY_AUTO_MEM_FRACTION", bad)
+        assert exact._query_chunk_rows(q, k) == 448
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda dev=None: (1 << 45, 1 << 46))
+    assert exact._query_chunk_rows(q, k) == 5000  # the 4 GiB cap holds 357913 rows: all 5000 fit
+    q_long = torch.zeros(1, 2, 10 ** 6, 128)
+    assert exact._query_chunk_rows(q_long, k) == ((4 << 30) // per_row) // 64 * 64
+
+    # the loop, with the score GEMM's output on the CPU and a count stand-in (no device here)
+    calls = []
+
+    def fake_counts(scores, scale, threshold):
+        calls.append(scores.shape[2])
+        if scores.shape[2] > 100:
+            raise torch.cuda.OutOfMemoryError("HIP out of memory")
+        return (scores.float() > 0).sum(-1).to(torch.int32)
+
+    monkeypatch.setattr(exact, "exact_counts_from_scores", fake_counts)
+    monkeypatch.setattr(exact, "_query_chunk_rows", lambda qq, kk: 448)
+    monkeypatch.setattr(torch.cuda, "empty_cache", lambda: None)
+    g = torch.Generator().manual_seed(0)
+    qq = torch.randn(1, 2, 1000, 128, generator=g).to(torch.bfloat16)
+    kk = torch.randn(1, 2, 300, 128, generator=g).to(torch.bfloat16)
+    monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: True))
+    avg, per_head, stats = exact.compute_exact_attention_sparsity(qq, kk)
+    assert calls[:3] == [448, 224, 112] and stats["chunk_size"] == 56
+    ref = (torch.matmul(qq, kk.transpose(-2, -1)).float() > 0).sum(-1).double() / 300
+    assert per_head == pytest.approx(ref.mean(dim=(0, 2)).tolist(), abs=1e-12)
+    calls.clear()
+    with pytest.raises(torch.cuda.OutOfMemoryError):
+        exact.compute_exact_attention_sparsity(qq, kk, batch_size=400)
 
 
 def test_sparsity_query_sampling_positions():
