@@ -154,7 +154,7 @@ def compute_exact_attention_sparsity(
     return avg, per_head.cpu().tolist(), stats
 
 
-def _resume_requested() -> bool:
+def resume_requested() -> bool:
     """``SVOO_SPARSITY_RESUME`` set to a true value (1, true, yes, on; any case) turns the resume guard on."""
     return os.environ.get("SVOO_SPARSITY_RESUME", "").strip().lower() in {"1", "true", "yes", "on"}
 
@@ -206,7 +206,7 @@ def _log_index(output_file: str) -> SparsityLogIndex:
 def has_completed_sparsity_entry(output_file: str, layer_idx: int, step: int, num_heads: int) -> bool:
     """Opt-in resume guard (``SVOO_SPARSITY_RESUME``): True when the raw log already holds every head of
     this layer/step, so the measurement can be skipped (``svoo/sparsity/exact.py:54-102``)."""
-    if not _resume_requested() or not output_file or not os.path.exists(output_file):
+    if not resume_requested() or not output_file or not os.path.exists(output_file):
         return False
     return _log_index(output_file).complete(layer_idx, step, num_heads)
 

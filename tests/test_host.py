@@ -256,6 +256,53 @@ def test_ear_row_params_matches_oracle(ratio):
     assert (pre, bpre) == ([0, 5, 34], [0, 10, 69])  # float32 reads of a tensor (0.35 -> 0.34999999)
 
 
+
+def test_replace_hunyuan_attention_numbers_double_then_single_blocks():
+    """HunyuanVideo 1.0 has 20 double-stream and 40 single-stream blocks; the profile CSV's layer index runs
+    over the double-stream blocks first (svoo/models/hunyuan10/inference.py:207-231)."""
+    from types import SimpleNamespace
+
+    from svoo_amd.inference import replace_hunyuan10_attention, replace_hunyuan_attention
+    from svoo_amd.processor import Hunyuan_SAPAttn_Processor
+
+    assert replace_hunyuan10_attention is replace_hunyuan_attention
+    blk = lambda: SimpleNamespace(attn=SimpleNamespace(processor=None))  # noqa: E731
+    pipe = SimpleNamespace(transformer=SimpleNamespace(transformer_blocks=[blk() for _ in range(20)],
+                                                       single_transformer_blocks=[blk() for _ in range(40)]))
+    cls = type("H", (Hunyuan_SAPAttn_Processor,), {})
+    procs = replace_hunyuan_attention(
+        pipe, 720, 1280, 129, prompt_length=200, first_layers_fp=0.025, first_times_fp=0.075, num_q_centroids=400,
+        num_k_centroids=1000, top_p_kmeans=0.9, min_kc_ratio=0.1, kmeans_iter_init=50, kmeans_iter_step=2,
+        context_length=512, start_reuse_step=11, reuse_interval=0, use_dynamic_min_kc_ratio=True,
+        sparsity_csv_path=str(GOLDEN / "sparsity_wan_1.3B_t2v_steps1-3.csv"), dynamic_min_kc_ratio_min=0.15,
+        dynamic_min_kc_ratio_max=0.2, processor_cls=cls)
+    assert [b.attn.processor.layer_idx for b in pipe.transformer.transformer_blocks] == list(range(20))
+    assert [b.attn.processor.layer_idx for b in pipe.transformer.single_transformer_blocks] == list(range(20, 60))
+    assert [p.layer_idx for p in procs] == list(range(60)) and all(type(p) is cls for p in procs)
+    # 129 frames -> 33 latent frames of 45 x 80 patches; the text context is fixed at 256 tokens
+    assert (cls.num_frame, cls.frame_size, cls.context_length, cls.prompt_length) == (33, 3600, 256, 200)
+    assert (cls.num_q_centroids, cls.num_k_centroids, cls.kmeans_iter_init, cls.kmeans_iter_step) == (400, 1000, 50, 2)
+    assert cls.reuse_interval == 1 and cls.start_reuse_step == 11 and cls.num_layers == 60
+    assert cls.use_dynamic_min_kc_ratio and cls.sparsity_lookup.get_sparsity(1, 0, 0) is not None
+    assert Hunyuan_SAPAttn_Processor.prompt_length == 0  # the base class is untouched
+    with pytest.raises(ValueError):
+        replace_hunyuan_attention(pipe, 720, 1280, 129, 10, 0, 0, pattern="SVG", processor_cls=cls)
+    with pytest.raises(ValueError):
+        replace_hunyuan_attention(pipe, 720, 1280, 129, 300, 0, 0, processor_cls=cls)  # prompt longer than the text
+    replace_hunyuan_attention(pipe, 720, 1280, 129, 10, 0, 0, use_dynamic_min_kc_ratio=True,
+                              sparsity_csv_path=str(GOLDEN / "missing.csv"), processor_cls=cls)
+    assert not cls.use_dynamic_min_kc_ratio and cls.sparsity_lookup is None
+
+
+def test_hunyuan_processor_rejects_prompt_longer_than_context():
+    from svoo_amd.processor import Hunyuan_SAPAttn_Processor
+
+    cls = type("H", (Hunyuan_SAPAttn_Processor,), {"prompt_length": 300, "context_length": 256, "num_frame": 1,
+                                                   "frame_size": 4})
+    x = torch.zeros(1, 2, 260, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="prompt_length"):
+        cls(layer_idx=0).attention_core_logic(x, x, x, None)
+
 def test_tiny_dit_dense_forward_shapes():
     from svoo_amd import dit
 
