@@ -159,6 +159,18 @@ int svoo_vbsa_fused_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         const int32_t* k_sorted_idx, const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes,
                         uint16_t* o_bshd, int bh, int heads, int s, int d, int qn, int kn, void* workspace,
                         size_t ws_bytes, int32_t* status, void* stream);
+/* svoo_vbsa_fused_fwd_noalloc: svoo_vbsa_fused_fwd without a workspace argument; it allocates nothing.
+ *   No counterpart in the reference.  It is for callers that cannot allocate device memory per call (code
+ *   under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The plan lives in a
+ *   static device array of SVOO_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call whose
+ *   plan (svoo_vbsa_workspace_size(bh, s, qn, kn)) exceeds it returns SVOO_ERR_WORKSPACE before any launch.
+ *   Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other
+ *   host threads) race and must be serialised by the caller. */
+#define SVOO_NOALLOC_SCRATCH_BYTES (4u << 20)
+int svoo_vbsa_fused_fwd_noalloc(const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* q_sorted_idx,
+                                const int32_t* k_sorted_idx, const uint8_t* map, const int32_t* q_sizes,
+                                const int32_t* k_sizes, uint16_t* o_bshd, int bh, int heads, int s, int d, int qn,
+                                int kn, int32_t* status, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * EAR (error-aware routing with centroid compensation).  All token inputs are cluster-contiguous

@@ -41,6 +41,8 @@ _SIGS = {
     "svoo_vbsa_segments": (c_int, [P, P, c_int, c_int, c_int, P, P, P, P]),
     "svoo_vbsa_fused_fwd": (c_int, [P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P, c_size_t,
                                     P, P]),
+    "svoo_vbsa_fused_fwd_noalloc": (c_int, [P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
+                                            P, P]),
     "svoo_probe_mfma_layout": (c_int, [P, P, P]),
     "svoo_probe_mfma_f64_layout": (c_int, [P, P]),
     "svoo_exact_sparsity_counts": (c_int, [P, c_longlong, c_int, c_float, c_float, P, P]),

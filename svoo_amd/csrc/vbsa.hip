@@ -25,6 +25,8 @@
 // EAR variant (centroid compensation): the KV stream continues after the active tokens with the
 // (key, value) centroids of the inactive clusters, each scored q . kc_j / sqrt(D) + log(|K_j| + 1e-6),
 // so one online softmax covers both (the reference's token attention + log-sum-exp merge).
+#include <mutex>
+
 #include "svoo_common.h"
 
 namespace svoo {
@@ -1014,6 +1016,58 @@ extern "C" int svoo_vbsa_fused_fwd(const uint16_t* q, const uint16_t* k, const u
                bh, heads);
   return vbsa_launch<false, true>("svoo_vbsa_fused_fwd", q, k, v, nullptr, nullptr, map, q_sizes, k_sizes, o_bshd, bh,
                                   s, d, qn, kn, workspace, ws_bytes, status, stream, q_sorted_idx, k_sorted_idx, heads);
+}
+
+// ------------------------------------------------------------------------------------------ allocation-free entry
+// svoo_vbsa_fused_fwd_noalloc keeps the plan (cluster offsets, work items, head order) in this file-scope
+// device array instead of a caller workspace.  Each device holds its own copy; host code must use the
+// address hipGetSymbolAddress returns for the current device, never the array's name.
+static __device__ __align__(256) unsigned char scratch[SVOO_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Address of `scratch` on the current device, resolved once per device.
+int scratch_on_current_device(const char* name, void** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  SVOO_REQUIRE(e == hipSuccess, SVOO_ERR_HIP, "%s: hipGetDevice failed: %s", name, hipGetErrorString(e));
+  SVOO_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, SVOO_ERR_UNSUPPORTED, "%s: device %d above %d", name, dev,
+               kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t es = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    SVOO_REQUIRE(es == hipSuccess && p, SVOO_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d failed: %s",
+                 name, dev, hipGetErrorString(es));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SVOO_OK;
+}
+}  // namespace
+
+extern "C" int svoo_vbsa_fused_fwd_noalloc(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                           const int32_t* q_sorted_idx, const int32_t* k_sorted_idx,
+                                           const uint8_t* map, const int32_t* q_sizes, const int32_t* k_sizes,
+                                           uint16_t* o_bshd, int bh, int heads, int s, int d, int qn, int kn,
+                                           int32_t* status, void* stream) {
+  static const char* name = "svoo_vbsa_fused_fwd_noalloc";
+  SVOO_REQUIRE(bh > 0 && s > 0 && qn > 0 && kn > 0, SVOO_ERR_INVALID_ARG, "%s: bad dims", name);
+  const size_t need = vbsa_layout(bh, s, qn, kn).total;
+  SVOO_REQUIRE(need <= (size_t)SVOO_NOALLOC_SCRATCH_BYTES, SVOO_ERR_WORKSPACE,
+               "%s: plan needs %zu bytes, above the static scratch of %zu bytes (use svoo_vbsa_fused_fwd with a "
+               "workspace)", name, need, (size_t)SVOO_NOALLOC_SCRATCH_BYTES);
+  SVOO_REQUIRE(q_sorted_idx && k_sorted_idx, SVOO_ERR_INVALID_ARG, "%s: null index", name);
+  SVOO_REQUIRE(heads > 0 && bh % heads == 0, SVOO_ERR_INVALID_ARG, "%s: bh=%d not a multiple of H=%d", name, bh,
+               heads);
+  void* ws = nullptr;
+  if (int rc = scratch_on_current_device(name, &ws)) return rc;
+  return vbsa_launch<false, true>(name, q, k, v, nullptr, nullptr, map, q_sizes, k_sizes, o_bshd, bh, s, d, qn, kn,
+                                  ws, (size_t)SVOO_NOALLOC_SCRATCH_BYTES, status, stream, q_sorted_idx, k_sorted_idx,
+                                  heads);
 }
 
 extern "C" int svoo_vbsa_ear_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* k_cent,

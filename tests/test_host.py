@@ -42,6 +42,21 @@ def test_library_reports_errors_without_launching():
     assert L.svoo_co_cluster_workspace_size(40, 75600, 100, 1000, 128) > 0
 
 
+def test_noalloc_attention_rejects_plans_above_its_scratch():
+    """The allocation-free attention checks its plan size against the static scratch before any HIP call."""
+    from svoo_amd import _lib
+
+    L = _lib.lib()
+    limit = 4 << 20  # SVOO_NOALLOC_SCRATCH_BYTES
+    assert L.svoo_vbsa_workspace_size(40, 75600, 100, 1000) <= limit  # the Wan2.1-14B 720p layer fits
+    bh = 2048
+    assert L.svoo_vbsa_workspace_size(bh, 75600, 100, 1000) > limit
+    rc = L.svoo_vbsa_fused_fwd_noalloc(1, 1, 1, 1, 1, 1, 1, 1, 1, bh, 1, 75600, 128, 100, 1000, None, None)
+    assert rc == -3 and "static scratch" in _lib.last_error()
+    rc = L.svoo_vbsa_fused_fwd_noalloc(1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 1, 75600, 128, 100, 1000, None, None)
+    assert rc == -1 and "bad dims" in _lib.last_error()
+
+
 def test_product_code_never_touches_the_oracle():
     for p in (ROOT / "svoo_amd").rglob("*.py"):
         text = p.read_text()
