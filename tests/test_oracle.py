@@ -146,6 +146,67 @@ def test_co_cluster_recovers_separated_mixture():
         O.co_cluster_tokens(q, k, 4, 4, 0, init_q_idx=init, init_k_idx=init)
 
 
+
+def _brute_labels(x, centroids, basis):
+    """Literal profile-space argmin in pure Python (svoo/co_clustering.py:2086-2255): the token's profile is its
+    dot products with the basis centroids, normalised with eps 1e-8 inside the root; a centroid's profile is the
+    bf16-rounded dot products with the basis, L2-normalised; the label minimises 2 - 2 <profiles>, first index
+    on ties."""
+    import math
+
+    def dot(a, b):
+        return math.fsum(float(u) * float(v) for u, v in zip(a, b))
+
+    prof = []
+    for c in centroids:
+        raw = [float(O.bf16_round(np.array([dot(c, b)], np.float32))[0]) for b in basis]
+        nrm = math.sqrt(math.fsum(r * r for r in raw) + 1e-8)
+        prof.append([r / nrm for r in raw])
+    labels = []
+    for t in x:
+        d = [dot(t, b) for b in basis]
+        nrm = math.sqrt(math.fsum(v * v for v in d) + 1e-8)
+        dist = [2.0 - 2.0 * math.fsum(v / nrm * pj for v, pj in zip(d, pr)) for pr in prof]
+        labels.append(min(range(len(dist)), key=lambda j: (dist[j], j)))
+    return np.array(labels)
+
+
+def test_co_cluster_wiring_key_step_then_query_step_on_new_key_centroids():
+    """Each iteration assigns keys in the space of the previous query centroids, updates the key centroids, then
+    assigns queries in the space of the *updated* key centroids (svoo/co_clustering.py:2423-2449).  The oracle's
+    trace shows each half-step's basis; a pure-Python brute force on a tiny case where a stale key-centroid
+    basis gives other query labels pins which one the oracle uses."""
+    rng = np.random.default_rng(77)
+    found = False
+    for attempt in range(200):
+        n, d, qn, kn = 12, 4, 3, 3
+        q = O.bf16_round(rng.standard_normal((1, n, d)).astype(np.float32))
+        k = O.bf16_round(rng.standard_normal((1, n, d)).astype(np.float32))
+        qi = rng.choice(n, size=(1, qn), replace=False)
+        ki = rng.choice(n, size=(1, kn), replace=False)
+        trace = []
+        ql, qc, qs, kl, kc, ks = O.co_cluster_tokens(q, k, qn, kn, 2, init_q_idx=qi, init_k_idx=ki, trace=trace)
+        assert [t[0] for t in trace] == ["k", "q", "k", "q"]
+        qc_run, kc_run = q[0, qi[0]], k[0, ki[0]]
+        for it in range(2):
+            (_, klab, _, kc_in, k_basis), (_, qlab, _, qc_in, q_basis) = trace[2 * it], trace[2 * it + 1]
+            np.testing.assert_array_equal(kc_in[0], kc_run)
+            np.testing.assert_array_equal(k_basis[0], qc_run)  # keys: previous query centroids
+            np.testing.assert_array_equal(klab[0], _brute_labels(k[0], kc_run, qc_run))
+            kc_new = O.centroid_update(k, klab, kc_in)[0][0]
+            np.testing.assert_array_equal(q_basis[0], kc_new)  # queries: the key centroids just updated
+            np.testing.assert_array_equal(qc_in[0], qc_run)
+            np.testing.assert_array_equal(qlab[0], _brute_labels(q[0], qc_run, kc_new))
+            stale = _brute_labels(q[0], qc_run, kc_run)
+            found = found or not np.array_equal(stale, qlab[0])
+            qc_run = O.centroid_update(q, qlab, qc_in)[0][0]
+            kc_run = kc_new
+        np.testing.assert_array_equal(qc[0], qc_run)
+        np.testing.assert_array_equal(kc[0], kc_run)
+        if found and attempt >= 4:
+            break
+    assert found, "no case where a stale key-centroid basis changes the query labels"
+
 def test_weighted_softmax_closed_forms():
     s = O.bf16_round(RNG.standard_normal((3, 50)).astype(np.float32))
     w = np.ones((3, 50))
