@@ -55,6 +55,8 @@ def parse_args():
                     help="time the offline profile producer (exact per-head sparsity of one layer) instead")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense SDPA comparator")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-kernel-table", action="store_true",
+                    help="skip the per-kernel table (one extra call under torch.profiler)")
     ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU baseline sample")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "vbsa_attn_C3_traffic.json"),
                     help="measured HBM traffic of the attention kernel (from rocprofv3 --pmc), if present")
@@ -198,6 +200,8 @@ def main():
             stage.setdefault(nm, []).append(e0.elapsed_time(e1))
     stages_ms = {nm: float(np.median(vals)) for nm, vals in stage.items()}
     attn_ms_avg = float(np.mean(stage["attention"]))
+    # each call's span from its first to its last stage mark (the same stream): the spread over the K calls
+    per_call = [ev[0][1].elapsed_time(ev[-1][1]) for ev in all_events]
 
     # Work of the last call (every call starts from the same centroids, so all calls are equal).
     last = proc._last_call
@@ -262,27 +266,46 @@ def main():
     del proc._step_from_callback
     log(f"reuse step {reuse_ms:.3f} ms")
 
-    # Dense comparator: SDPA at equal shape (flash / memory-efficient kernels only).
-    t_sdpa_ms = None
+    # Dense comparators at equal shape, each timed per repetition: torch SDPA (flash / memory-efficient kernels
+    # only, the reference's dense path) and this library's attention kernel on an all-true one-cluster map.
+    def timed_reps(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        out_ms = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            out_ms.append(a.elapsed_time(b))
+        return out_ms
+
+    sdpa_reps, own_reps = None, None
     if not args.no_dense:
         try:
             from torch.nn.attention import SDPBackend, sdpa_kernel
 
             with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-                o = torch.nn.functional.scaled_dot_product_attention(q, k, v)
-                torch.cuda.synchronize()
-                ds, de = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                reps = 2
-                ds.record()
-                for _ in range(reps):
-                    o = torch.nn.functional.scaled_dot_product_attention(q, k, v)
-                de.record()
-                torch.cuda.synchronize()
-                t_sdpa_ms = ds.elapsed_time(de) / reps
-                del o
-            log(f"dense SDPA {t_sdpa_ms:.2f} ms")
+                sdpa_reps = timed_reps(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v), 3)
+            log(f"dense SDPA {np.median(sdpa_reps):.2f} ms (reps {[round(x, 2) for x in sdpa_reps]})")
         except Exception as e:  # the comparator is informative only
             log(f"dense SDPA comparator unavailable: {e!r}")
+        from svoo_amd.co_clustering import dynamic_block_sparse_fwd
+
+        full_sz = torch.full((1, h, 1), n, dtype=torch.int32, device=dev)
+        full_map = torch.ones(1, h, 1, 1, dtype=torch.bool, device=dev)
+        own_reps = timed_reps(lambda: dynamic_block_sparse_fwd(q, k, v, full_map, full_sz, full_sz, validate=False), 3)
+        log(f"dense (this library's kernel, all-true map) {np.median(own_reps):.2f} ms")
+    t_sdpa_ms = None if sdpa_reps is None else float(np.median(sdpa_reps))
+    t_own_ms = None if own_reps is None else float(np.median(own_reps))
+
+    kernels = None
+    if not args.no_kernel_table:
+        try:
+            kernels = kernel_table(step, cfg, h, nv, d, qcn, kcn, iters)
+        except Exception as e:  # informative only
+            log(f"per-kernel table unavailable: {e!r}")
 
     traffic = None
     tpath = Path(args.traffic)
@@ -339,12 +362,93 @@ def main():
         "permute_gbps": round(permute_bytes / (permute_ms * 1e-3) / 1e9, 1),
         "permutes_fused_into_attention": permute_fused,
         "permute_frac_hbm": round(permute_bytes / (permute_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "call_ms_spread": {"min": round(min(per_call), 4), "median": round(float(np.median(per_call)), 4),
+                           "max": round(max(per_call), 4), "calls": len(per_call)},
         "t_sdpa_ms": None if t_sdpa_ms is None else round(t_sdpa_ms, 3),
+        "t_sdpa_ms_reps": None if sdpa_reps is None else [round(x, 3) for x in sdpa_reps],
         "speedup_vs_dense": None if t_sdpa_ms is None else round(t_sdpa_ms / t_call_ms, 3),
+        "speedup_vs_dense_spread": None if sdpa_reps is None else {
+            "min": round(min(sdpa_reps) / max(per_call), 3), "max": round(max(sdpa_reps) / min(per_call), 3)},
+        "t_dense_own_kernel_ms": None if t_own_ms is None else round(t_own_ms, 3),
+        "dense_own_kernel_tflops": None if t_own_ms is None else round(dense_flop / (t_own_ms * 1e-3) / 1e12, 1),
+        "speedup_vs_dense_own_kernel": None if t_own_ms is None else round(t_own_ms / t_call_ms, 3),
+        "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def kernel_table(step, cfg, h, nv, d, qcn, kcn, iters):
+    """Device time of every kernel of one call, from one extra call under torch.profiler (outside the timed
+    region), and roofline figures for the clustering kernels: the assignment's key side (J = Kc, MFMA bound:
+    2*d*J FLOP per token of the reduced form) and query side (J = Qc, HBM bound: a 256-byte token row read and
+    a 4-byte label written), the sorted centroid sums (HBM: the row, its index and label per token) and the
+    incremental update.  Launch order inside the co-clustering alternates key side, query side."""
+    import torch
+    from torch.profiler import ProfilerActivity, profile
+
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        step()
+        torch.cuda.synchronize()
+    evs = [e for e in prof.events() if getattr(e, "device_type", None) is not None
+           and str(e.device_type).endswith("CUDA") and e.time_range.elapsed_us() > 0]
+    evs.sort(key=lambda e: e.time_range.start)
+
+    def short(name):
+        base = name.split("(")[0].replace("void ", "").strip()
+        return base.split("::")[-1].split("<")[0]
+
+    table = {}
+    for e in evs:
+        t = table.setdefault(short(e.name), {"count": 0, "total_us": 0.0})
+        t["count"] += 1
+        t["total_us"] += e.time_range.elapsed_us()
+    for t in table.values():
+        t["avg_us"] = round(t["total_us"] / t["count"], 2)
+        t["total_us"] = round(t["total_us"], 1)
+
+    def launches(name):
+        return [e.time_range.elapsed_us() for e in evs if short(e.name) == name]
+
+    out = {"per_kernel": dict(sorted(table.items(), key=lambda kv: -kv[1]["total_us"]))}
+    bh = h
+    stage = {}
+    for nm in ("cocluster_assign16_kernel", "cocluster_assign_kernel"):
+        ts = launches(nm)
+        if ts:
+            stage[nm] = {"key_side_avg_us": round(float(sum(ts[0::2]) / len(ts[0::2])), 2),
+                         "query_side_avg_us": round(float(sum(ts[1::2]) / max(1, len(ts[1::2]))), 2)}
+    a16 = launches("cocluster_assign16_kernel")
+    fb = launches("cocluster_assign_kernel")
+    if a16:
+        key_us = (sum(a16[0::2]) + sum(fb[0::2])) / len(a16[0::2])
+        qry_us = (sum(a16[1::2]) + sum(fb[1::2])) / max(1, len(a16[1::2]))
+        key_flop = 2.0 * bh * nv * d * kcn
+        qry_bytes = bh * nv * (2 * d + 4)
+        stage["assign_key_side"] = {"bound": "mfma", "achieved": round(key_flop / (key_us * 1e-6) / 1e12, 1),
+                                    "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                    "frac": round(key_flop / (key_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                                    "avg_us_per_side": round(key_us, 2),
+                                    "note": "fp16 certified pass + hi/lo fallback; algorithmic FLOP of the reduced form"}
+        stage["assign_query_side"] = {"bound": "hbm", "achieved": round(qry_bytes / (qry_us * 1e-6) / 1e9, 1),
+                                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                                      "frac": round(qry_bytes / (qry_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                                      "avg_us_per_side": round(qry_us, 2)}
+    acc = launches("centroid_accumulate_kernel")
+    if acc:
+        acc_bytes = [bh * nv * (2 * d + 8)] * len(acc)
+        ach = sum(acc_bytes) / (sum(acc) * 1e-6) / 1e9
+        stage["centroid_accumulate"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                                        "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                                        "avg_us": round(sum(acc) / len(acc), 2)}
+    dl = launches("centroid_delta_kernel")
+    if dl:
+        stage["centroid_delta"] = {"avg_us": round(sum(dl) / len(dl), 2), "launches": len(dl),
+                                   "note": "moves only the tokens whose label changed"}
+    out["clustering"] = stage
+    return out
 
 
 def main_dit(args):

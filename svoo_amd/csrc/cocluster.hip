@@ -18,6 +18,21 @@ namespace svoo {
 
 constexpr int kPrepMaxLds = 52 * 1024;  // LDS budget of the prep kernel's profile rows
 constexpr int kAssignChunk = 64;   // E rows staged in LDS per step
+// Shared counters (per-head fallback counts, the two change counters) sit 256 bytes apart, each on a cache
+// line of its own, and every wave reserves all the slots it needs with one atomic: thousands of waves adding
+// one by one to counters on one line serialise in the L2.
+constexpr int kCounterStride = 64;  // int32 elements
+
+// One atomicAdd per wave on `counter` for `count` slots (wave-uniform); the base slot in every lane.
+__device__ __forceinline__ int wave_reserve(int32_t* counter, int count) {
+  int base = 0;
+  if (count > 0 && (threadIdx.x % kWave) == 0) base = atomicAdd(counter, count);
+  return __shfl(base, 0);
+}
+// Rank of this lane among the set lanes of a wave mask below it.
+__device__ __forceinline__ int mask_rank(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+}
 
 // --------------------------------------------------------------------------------------- prep
 // kPrepRows rows of A per block: 8 when there are many rows (the key side) and the profile width
@@ -158,7 +173,9 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
                                                                   uint16_t* __restrict__ e_hi,
                                                                   uint16_t* __restrict__ e_lo,
                                                                   float* __restrict__ profile, int j, int kp,
-                                                                  int jpad) {
+                                                                  int jpad, uint16_t* __restrict__ e16,
+                                                                  uint32_t* __restrict__ err_max,
+                                                                  uint32_t* __restrict__ norm_max) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int kpp = pm_kpp(kp), ps = kpp + 2;
   uint16_t* praw = (uint16_t*)smem;                             // [16][ps] bf16
@@ -219,12 +236,15 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
   // Phase 3.
   f64x4_t e0 = {0.0, 0.0, 0.0, 0.0}, e1 = {0.0, 0.0, 0.0, 0.0};
   const int dd0 = 32 * wave + li, dd1 = dd0 + 16;
+  uint32_t bmax = 0;  // max |B| as bf16 magnitude bits (they order like the values)
   for (int c = 0; c < kpp; c += kPmChunk) {
     __syncthreads();  // the previous chunk is consumed
     for (int t = tid; t < kPmChunk * 16; t += 256) {
       const int row = t / 16, piece = t % 16;
-      *(u32x4_t*)(bch + row * kPmChunkStride + piece * 8) =
-          *((const u32x4_t*)(bb + (size_t)min(c + row, kp - 1) * 128) + piece);
+      const u32x4_t w = *((const u32x4_t*)(bb + (size_t)min(c + row, kp - 1) * 128) + piece);
+      *(u32x4_t*)(bch + row * kPmChunkStride + piece * 8) = w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bmax = max(bmax, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
     }
     __syncthreads();
 #pragma unroll 4
@@ -237,9 +257,30 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
   }
   uint16_t* hb = e_hi + (size_t)bidx * jpad * 128;
   uint16_t* lb = e_lo + (size_t)bidx * jpad * 128;
+  // fp16 copy for the certified single-pass assignment: E * 2^t with one power of two per head, chosen
+  // from an a-priori bound so that no element overflows (|E_ji| <= |P_j| |B_.i| <= sqrt(kp) max|B|, and
+  // |P_j| <= 1): every block of the head derives the same t from max|B|.
+  int t_scale = 0;
+  if (e16) {
+    __syncthreads();  // every thread is done with bch
+    uint32_t* red = (uint32_t*)bch;
+    for (int o = 32; o > 0; o >>= 1) bmax = max(bmax, (uint32_t)__shfl_xor((int)bmax, o));
+    if (lane == 0) red[wave] = bmax;
+    __syncthreads();
+    bmax = max(max(red[0], red[1]), max(red[2], red[3]));
+    __syncthreads();
+    if (bmax) {
+      int ex;
+      frexp(sqrt((double)kp) * (double)bf16_to_f32((uint16_t)bmax), &ex);  // bound < 2^ex
+      t_scale = 15 - ex;
+    }
+  }
+  float err2[4], nrm2[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int i = 4 * v + q, row = r0 + i;
+    err2[v] = 0.0f;
+    nrm2[v] = 0.0f;
     if (row >= jpad) continue;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
@@ -249,6 +290,55 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
       const int dd = hh ? dd1 : dd0;
       hb[(size_t)row * 128 + dd] = hi;
       lb[(size_t)row * 128 + dd] = lo;
+      if (e16) {
+        // padding rows (row >= j) are zero in the fp16 copy: their score is exactly 0
+        const double es = row < j ? ldexp(e, t_scale) : 0.0;
+        const _Float16 h16 = (_Float16)(float)es;
+        const double err = es - (double)(float)h16;  // exact
+        err2[v] += (float)(err * err);
+        nrm2[v] += (float)((double)(float)h16 * (double)(float)h16);
+        e16[((size_t)bidx * jpad + row) * 128 + dd] = __builtin_bit_cast(uint16_t, h16);
+      }
+    }
+  }
+  if (e16) {
+    // Per-row |2^t E_j - E16_j| and |E16_j| (rows of real clusters only), then the head's maxima.  A row's 128
+    // columns are spread over the 16 lanes of a lane quarter in each of the 4 waves.
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        err2[v] += __shfl_xor(err2[v], o);
+        nrm2[v] += __shfl_xor(nrm2[v], o);
+      }
+    float* part = (float*)bch;  // [wave][row][2]
+    if (li == 0)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        part[(wave * 16 + 4 * v + q) * 2] = err2[v];
+        part[(wave * 16 + 4 * v + q) * 2 + 1] = nrm2[v];
+      }
+    __syncthreads();
+    if (tid < 16) {
+      const int i = tid;
+      float er = 0.0f, nr = 0.0f;
+      if (r0 + i < j)
+        for (int w = 0; w < 4; ++w) {
+          er += part[(w * 16 + i) * 2];
+          nr += part[(w * 16 + i) * 2 + 1];
+        }
+      // rounded-to-nearest fp32 sums of at most 128 squares: 2^-17 relative slack covers their rounding
+      er = sqrtf(er * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
+      nr = sqrtf(nr * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) {
+        er = fmaxf(er, __shfl_xor(er, o));
+        nr = fmaxf(nr, __shfl_xor(nr, o));
+      }
+      if (tid == 0) {
+        atomicMax(err_max + bidx, __float_as_uint(er));
+        atomicMax(norm_max + bidx, __float_as_uint(nr));
+      }
     }
   }
 }
@@ -265,15 +355,30 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
 constexpr int kAsgTokWave = 128;
 constexpr int kAsgTok = 4 * kAsgTokWave;
 
+// With LIST the block's tokens are entries [512 x, 512 x + 512) of the head's token list (list[bidx][.],
+// count[bidx] entries; blocks past the count exit at once): the tokens the certified fp16 pass could not
+// settle.
+template <bool LIST>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi,
                         const uint16_t* __restrict__ e_lo, int32_t* __restrict__ labels, int n, int j, int jpad,
-                        int2* __restrict__ changes, int32_t* __restrict__ nchanges) {
+                        int2* __restrict__ changes, int32_t* __restrict__ nchanges,
+                        const int32_t* __restrict__ list, const int32_t* __restrict__ list_count) {
   __shared__ __attribute__((aligned(16))) uint16_t s_e[2][2][kAssignChunk * 128];  // [buffer][hi, lo]
   const int bidx = blockIdx.y;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int h = lane / 32, l32 = lane % 32;
   const int tok0 = blockIdx.x * kAsgTok + wave * kAsgTokWave;
+  const int ntok = LIST ? list_count[(size_t)bidx * kCounterStride] : n;  // positions < ntok hold tokens
+  if (LIST && (int)blockIdx.x * kAsgTok >= ntok) return;
+  const int32_t* lst = LIST ? list + (size_t)bidx * n : nullptr;
+  // token at position p of this block's range (positions past the range load a valid row, unused)
+  auto token_at = [&](int pos) __attribute__((always_inline)) -> int {
+    if constexpr (LIST)
+      return lst[min(pos, ntok - 1)];
+    else
+      return min(pos, n - 1);
+  };
   const uint16_t* xb = x + (size_t)bidx * n * 128;
   const uint16_t* hb = e_hi + (size_t)bidx * jpad * 128;
   const uint16_t* lb = e_lo + (size_t)bidx * jpad * 128;
@@ -297,7 +402,7 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   u32x4_t xop[4][8];
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
-    const int row = min(tok0 + cb * 32 + l32, n - 1);
+    const int row = token_at(tok0 + cb * 32 + l32);
     const u32x4_t* src = (const u32x4_t*)(xb + (size_t)row * 128);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) xop[cb][ks] = src[ks * 2 + h];
@@ -371,6 +476,9 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
     const int r = 15 - (int)(__float_as_uint(best_v[cb]) & 15u);
     best_j[cb] += (r / 4) * 8 + (r % 4) + h * 4;
   }
+  int lab[4], oldl[4], tokv[4];
+  uint64_t chm[4];
+  int nch_wave = 0;
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
     // the two halves of a token: larger score, then lower row
@@ -380,17 +488,251 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
       best_s[cb] = ov;
       best_j[cb] = oj;
     }
-    const int tok = tok0 + cb * 32 + l32;
+    const int pos = tok0 + cb * 32 + l32;
+    const bool mine = h == 0 && pos < ntok;
+    tokv[cb] = mine ? token_at(pos) : -1;
     // padding rows repeat row j - 1: a padding winner stands for row j - 1
-    if (h == 0 && tok < n) {
-      const int nl = min(best_j[cb], j - 1);
-      int32_t* lp = labels + (size_t)bidx * n + tok;
-      if (nchanges) {  // labels holds the previous iteration's labels: list the changes
-        const int ol = *lp;
-        if (ol != nl) changes[atomicAdd(nchanges, 1)] = make_int2(bidx * n + tok, (ol << 16) | nl);
-      }
-      *lp = nl;
+    lab[cb] = min(best_j[cb], j - 1);
+    // labels holds the previous iteration's labels when the changes are listed
+    oldl[cb] = (mine && nchanges) ? labels[(size_t)bidx * n + tokv[cb]] : lab[cb];
+    chm[cb] = __ballot(mine && oldl[cb] != lab[cb]);
+    nch_wave += (int)__popcll(chm[cb]);
+  }
+  const int cbase = nchanges ? wave_reserve(nchanges, nch_wave) : 0;
+  int cpre = 0;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    if (tokv[cb] >= 0) {
+      if (oldl[cb] != lab[cb])
+        changes[cbase + cpre + mask_rank(chm[cb])] = make_int2(bidx * n + tokv[cb], (oldl[cb] << 16) | lab[cb]);
+      labels[(size_t)bidx * n + tokv[cb]] = lab[cb];
     }
+    cpre += (int)__popcll(chm[cb]);
+  }
+}
+
+// --------------------------------------------------------------------------------------- certified fp16 assign
+// One MFMA pass in fp16 instead of the two bf16 passes (E_hi, E_lo), with a rigorous error bound.
+//   * Token x is scaled by a power of two 2^u (its largest |component| into [2^14, 2^15)) and rounded
+//     to fp16 with round-toward-zero: bf16 values in that range are exact in fp16, and components below
+//     2^-17 (scaled) move by less than 2^-24 each.  E16 = fp16(2^t E) (prep; one t per head).
+//   * s~_j = x~ . E16_j on v_mfma_f32_32x32x16_f16 (exact fp16 products, fp32 sums).  For the scaled exact
+//     score S_j = 2^(u+t) x . E_j:  |S_j - s~_j| <= |x~| (D + 2^-17 Emax) + 2^-20 (Emax + D)
+//     with D = max_j |2^t E_j - E16_j| and Emax = max_j |E16_j| (prep measures both per head), the fp32
+//     sum bound 128 * 2^-24 |x~||E16_j| and the token rounding |2^u x - x~| < 2^-20.5.  The tag in the
+//     low 4 mantissa bits moves a score by < 2^-19 |s~|.  With |x~| >= 2^14 all of it is below
+//     B = |x~| (D + 2^-15 Emax).
+//   * The label is certified when the best score exceeds the second by more than 2 B: then it is the
+//     exact argmax of x . E (no tie is possible).  Other tokens (near-equal top scores, a zero token) go
+//     to the head's fallback list for the hi + lo kernel, which also applies its tie rule.
+// Each lane keeps the top two tagged scores of its cluster rows (median-of-three update) and the tile of
+// the best.  Padding rows (j .. jpad-1) are zero in E16, so they score exactly 0: as the runner-up such a
+// row only tightens the test, and a token whose best row is padding goes to the fallback.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f16x8_t as_f16x8(u32x4_t v) { return __builtin_bit_cast(f16x8_t, v); }
+__device__ __forceinline__ f32x16_t mfma32x32x16_f16(f16x8_t a, f16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ e16,
+                          const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max,
+                          int32_t* __restrict__ labels, int n, int j, int jpad, int2* __restrict__ changes,
+                          int32_t* __restrict__ nchanges, int32_t* __restrict__ fb_list,
+                          int32_t* __restrict__ fb_count) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_e[2][kAssignChunk * 128];
+  const int bidx = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int h = lane / 32, l32 = lane % 32;
+  const int tok0 = blockIdx.x * kAsgTok + wave * kAsgTokWave;
+  const uint16_t* xb = x + (size_t)bidx * n * 128;
+  const uint16_t* eb = e16 + (size_t)bidx * jpad * 128;
+  const int nchunks = jpad / kAssignChunk;
+
+  const int prow = lane / 16, pch = lane % 16;
+  auto issue = [&](int c, int bf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int r = 16 * wave + 4 * g + prow;
+      lds_dma16(eb + (size_t)(c * kAssignChunk + r) * 128 + swz(r, pch) * 8, &s_e[bf][(16 * wave + 4 * g) * 128]);
+    }
+  };
+  issue(0, 0);
+
+  // Tokens: fp16, scaled per token.
+  u32x4_t xop[4][8];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int row = min(tok0 + cb * 32 + l32, n - 1);
+    const u32x4_t* src = (const u32x4_t*)(xb + (size_t)row * 128);
+    u32x4_t raw[8];
+    uint32_t mbits = 0;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      raw[ks] = src[ks * 2 + h];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mbits = max(mbits, max(raw[ks][e] & 0x7fffu, (raw[ks][e] >> 16) & 0x7fffu));
+    }
+    mbits = max(mbits, (uint32_t)__shfl_xor((int)mbits, 32));
+    // biased exponent of the largest component (subnormals count as exponent -126)
+    const int be = max(1, (int)(mbits >> 7));
+    const int u = mbits ? 14 - (be - 127) : 0;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __builtin_amdgcn_ldexpf(bf16_to_f32((uint16_t)(raw[ks][e] & 0xffffu)), u);
+        const float hi = __builtin_amdgcn_ldexpf(bf16_to_f32((uint16_t)(raw[ks][e] >> 16)), u);
+        xop[cb][ks][e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+      }
+  }
+  const int sw = swz(l32, 0), g = sw >> 1;
+  const int abase = l32 * 128 + 8 * (h ^ (sw & 1));
+#define AOFF(ks) (abase + 16 * ((ks) ^ g))
+
+  float top1[4], top2[4];
+  int tbase[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    top1[cb] = -INFINITY;
+    top2[cb] = -INFINITY;
+    tbase[cb] = 0;
+  }
+  // +inf the optimiser cannot see (a visible one folds med3(x, t, +inf) back into a max with NaN quieting)
+  uint32_t pinf_bits;
+  __asm__ volatile("s_mov_b32 %0, 0x7f800000" : "=s"(pinf_bits));
+  const float pinf = __uint_as_float(pinf_bits);
+  f32x16_t acc[4];
+  // Top-two update of token block cb with tile jb: per score a tag, a median of three and a max (written as a
+  // median with +inf: fmaxf on bit-cast values would add a NaN-quieting instruction per score).
+  auto epi = [&](int cb, int jb) __attribute__((always_inline)) {
+    const float prev = top1[cb];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float t = __uint_as_float((__float_as_uint(acc[cb][r]) & ~15u) | (uint32_t)(15 - r));
+      top2[cb] = __builtin_amdgcn_fmed3f(top1[cb], top2[cb], t);
+      top1[cb] = __builtin_amdgcn_fmed3f(top1[cb], t, pinf);
+    }
+    tbase[cb] = top1[cb] != prev ? jb : tbase[cb];
+  };
+  // Two token blocks' MFMAs, their accumulator chains interleaved (a chain's next MFMA waits on the previous),
+  // with the A operands (E16 rows of the 32-row tile) read from LDS two k-steps ahead into a ring of three.
+  auto mfmas2 = [&](int cb0, const uint16_t* tile) __attribute__((always_inline)) {
+    u32x4_t ring[3];
+    ring[0] = *(const u32x4_t*)(tile + AOFF(0));
+    ring[1] = *(const u32x4_t*)(tile + AOFF(1));
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      acc[cb0] = mfma32x32x16_f16(as_f16x8(ring[ks % 3]), as_f16x8(xop[cb0][ks]), ks ? acc[cb0] : f32x16_t{});
+      if (ks + 2 < 8) ring[(ks + 2) % 3] = *(const u32x4_t*)(tile + AOFF(ks + 2));
+      acc[cb0 + 1] =
+          mfma32x32x16_f16(as_f16x8(ring[ks % 3]), as_f16x8(xop[cb0 + 1][ks]), ks ? acc[cb0 + 1] : f32x16_t{});
+    }
+  };
+  // Software pipeline within the wave: the MFMAs of blocks {0, 1} run while the VALU updates the top two of
+  // blocks {2, 3} of the previous 32-row tile, then the MFMAs of {2, 3} beside the updates of {0, 1}; per k-step
+  // an MFMA, six VALU instructions, the LDS read two k-steps ahead, an MFMA, six VALU instructions.
+  auto interleave = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      if (i + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+    }
+  };
+  // Before the first tile the pending updates of blocks 2 and 3 see scores of -FLT_MAX, below every real score
+  // (|s~| < 2^38), so they change nothing that survives; the update needs no branch (a branch would split the
+  // scheduling region and keep the VALU work away from the MFMAs).
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    acc[2][r] = -3.402823466e38f;
+    acc[3][r] = -3.402823466e38f;
+  }
+  int pend_jb = 0;
+  for (int c = 0; c < nchunks; ++c) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (c + 1 < nchunks) issue(c + 1, (c + 1) & 1);
+    const uint16_t* se = s_e[c & 1];
+#pragma unroll
+    for (int rb = 0; rb < kAssignChunk / 32; ++rb) {
+      const uint16_t* tile = se + rb * 32 * 128;
+      const int jb = c * kAssignChunk + rb * 32;
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas2(0, tile);
+      epi(2, pend_jb);
+      epi(3, pend_jb);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas2(2, tile);
+      epi(0, jb);
+      epi(1, jb);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+      pend_jb = jb;
+    }
+  }
+  epi(2, pend_jb);
+  epi(3, pend_jb);
+#undef AOFF
+  const float dd = __uint_as_float(err_max[bidx]), em = __uint_as_float(norm_max[bidx]);
+  const float slack = dd + 0x1p-15f * em;
+  int lab[4], oldl[4];
+  bool certv[4], minev[4];
+  uint64_t fbm[4], chm[4];
+  int nfb = 0, nch_wave = 0;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    // |x~| of the fp16 operands themselves (fp32 sum of 128 exact squares; 1.001 below covers its rounding)
+    float n2 = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const auto hv = __builtin_bit_cast(_Float16 __attribute__((ext_vector_type(2))), xop[cb][ks][e]);
+        const float lo = (float)hv[0], hi = (float)hv[1];
+        n2 = fmaf(lo, lo, fmaf(hi, hi, n2));
+      }
+    n2 += __shfl_xor(n2, 32);
+    const float xnorm = sqrtf(n2);
+    const int r = 15 - (int)(__float_as_uint(top1[cb]) & 15u);
+    const int jbest = tbase[cb] + (r / 4) * 8 + (r % 4) + h * 4;
+    const float s1 = __uint_as_float(__float_as_uint(top1[cb]) & ~15u);
+    const float s2 = __uint_as_float(__float_as_uint(top2[cb]) & ~15u);
+    const float o1 = __shfl_xor(s1, 32), o2 = __shfl_xor(s2, 32);
+    const int oj = __shfl_xor(jbest, 32);
+    const float best = fmaxf(s1, o1);
+    const float second = fmaxf(fminf(s1, o1), fmaxf(s2, o2));
+    lab[cb] = s1 >= o1 ? jbest : oj;
+    const float bound = xnorm * slack * 1.001f;
+    // a padding row (score 0) as the second only makes the test stricter; as the best it is not a label
+    certv[cb] = (best - second) > 2.0f * bound && lab[cb] < j;  // false for NaN
+    const int tok = tok0 + cb * 32 + l32;
+    minev[cb] = h == 0 && tok < n;
+    fbm[cb] = __ballot(minev[cb] && !certv[cb]);
+    // labels holds the previous iteration's labels when the changes are listed
+    oldl[cb] = (minev[cb] && certv[cb] && nchanges) ? labels[(size_t)bidx * n + tok] : lab[cb];
+    chm[cb] = __ballot(minev[cb] && certv[cb] && oldl[cb] != lab[cb]);
+    nfb += (int)__popcll(fbm[cb]);
+    nch_wave += (int)__popcll(chm[cb]);
+  }
+  const int fbase = wave_reserve(fb_count + (size_t)bidx * kCounterStride, nfb);
+  const int cbase = nchanges ? wave_reserve(nchanges, nch_wave) : 0;
+  int fpre = 0, cpre = 0;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int tok = tok0 + cb * 32 + l32;
+    if (minev[cb] && !certv[cb]) fb_list[(size_t)bidx * n + fbase + fpre + mask_rank(fbm[cb])] = tok;
+    if (minev[cb] && certv[cb]) {
+      if (oldl[cb] != lab[cb])
+        changes[cbase + cpre + mask_rank(chm[cb])] = make_int2(bidx * n + tok, (oldl[cb] << 16) | lab[cb]);
+      labels[(size_t)bidx * n + tok] = lab[cb];
+    }
+    fpre += (int)__popcll(fbm[cb]);
+    cpre += (int)__popcll(chm[cb]);
   }
 }
 
@@ -417,11 +759,14 @@ static size_t prep_smem(int rows, int kp) {
   return (size_t)rows * 128 * sizeof(double) + rows * sizeof(double) + (size_t)rows * kp * sizeof(float);
 }
 
+// With e16 (only for kp <= kPmMaxKp, the fp64-MFMA kernel) also the fp16 copy and the per-head error maxima
+// (err_max / norm_max must be zero on entry).
 static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uint16_t* e_lo, float* profile, int bh,
-                       int j, int kp, int jpad, hipStream_t stream) {
+                       int j, int kp, int jpad, hipStream_t stream, uint16_t* e16 = nullptr,
+                       uint32_t* err_max = nullptr, uint32_t* norm_max = nullptr) {
   if (kp <= kPmMaxKp) {
     hipLaunchKernelGGL(cocluster_prep_mfma_kernel, dim3(jpad / kPmRows, bh), dim3(256), pm_smem(kp), stream, a, b,
-                       e_hi, e_lo, profile, j, kp, jpad);
+                       e_hi, e_lo, profile, j, kp, jpad, e16, err_max, norm_max);
     return check_launch("svoo_cocluster_prep");
   }
   // Wide profiles: the vector kernel.  Few rows -> 2 rows per block for more blocks; many -> 8.
@@ -436,11 +781,28 @@ static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uin
 }
 
 static int assign_launch(const uint16_t* x, const uint16_t* e_hi, const uint16_t* e_lo, int32_t* labels, int bh, int n,
-                         int j, int jpad, hipStream_t stream, int2* changes = nullptr, int32_t* nchanges = nullptr) {
+                         int j, int jpad, hipStream_t stream, int2* changes = nullptr, int32_t* nchanges = nullptr,
+                         const int32_t* list = nullptr, const int32_t* list_count = nullptr) {
   dim3 grid((n + kAsgTok - 1) / kAsgTok, bh);
-  hipLaunchKernelGGL(cocluster_assign_kernel, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad, changes,
-                     nchanges);
+  if (list)
+    hipLaunchKernelGGL(cocluster_assign_kernel<true>, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad,
+                       changes, nchanges, list, list_count);
+  else
+    hipLaunchKernelGGL(cocluster_assign_kernel<false>, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad,
+                       changes, nchanges, nullptr, nullptr);
   return check_launch("svoo_cocluster_assign");
+}
+
+// The certified fp16 pass, then the hi + lo kernel on the tokens it left (fb_count must be zero on entry).
+static int assign16_launch(const uint16_t* x, const uint16_t* e16, const uint16_t* e_hi, const uint16_t* e_lo,
+                           const uint32_t* err_max, const uint32_t* norm_max, int32_t* labels, int bh, int n, int j,
+                           int jpad, int32_t* fb_list, int32_t* fb_count, hipStream_t stream, int2* changes,
+                           int32_t* nchanges) {
+  dim3 grid((n + kAsgTok - 1) / kAsgTok, bh);
+  hipLaunchKernelGGL(cocluster_assign16_kernel, grid, dim3(256), 0, stream, x, e16, err_max, norm_max, labels, n, j,
+                     jpad, changes, nchanges, fb_list, fb_count);
+  if (int rc = check_launch("svoo_co_cluster (fp16 assign)")) return rc;
+  return assign_launch(x, e_hi, e_lo, labels, bh, n, j, jpad, stream, changes, nchanges, fb_list, fb_count);
 }
 
 static const int kMaxClusters = 4096;
@@ -474,9 +836,13 @@ extern "C" int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, co
 //   sorted_lab   [bh][n] int32
 //   sums_q       [bh][qc][128] fp64          (query-centroid sums)
 //   changes      [bh * n] int2               (label changes of one assignment: token, old << 16 | new)
-//   nchanges     2 int32                     (change counters, key and query side)
+//   nchanges     2 int32, 256 bytes apart    (change counters, key and query side)
+//   e16          [bh][jpad_max][128] fp16    (the certified single-pass copy of E)
+//   fb_list      [bh][n] int32               (tokens the fp16 pass left to the hi + lo kernel)
+//   stats        [bh] x 256 B + 2 x [bh]    (fallback counts 256 bytes apart, max |2^t E - E16|, max |E16|)
 struct CoClusterWs {
-  size_t e_off, counts_off, sums_off, slab_off, sums_q_off, changes_off, nchanges_off, total;
+  size_t e_off, counts_off, sums_off, slab_off, sums_q_off, changes_off, nchanges_off, e16_off, fb_off, stats_off,
+      total;
 };
 
 static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
@@ -493,7 +859,10 @@ static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
   w.sums_q_off = w.slab_off + al((size_t)bh * n * sizeof(int32_t));
   w.changes_off = w.sums_q_off + al((size_t)bh * qc * 128 * sizeof(double));
   w.nchanges_off = w.changes_off + al((size_t)bh * n * sizeof(int2));
-  w.total = w.nchanges_off + 256;
+  w.e16_off = w.nchanges_off + al(2 * kCounterStride * sizeof(int32_t));
+  w.fb_off = w.e16_off + e_bytes;
+  w.stats_off = w.fb_off + al((size_t)bh * n * sizeof(int32_t));
+  w.total = w.stats_off + al((size_t)(kCounterStride + 2) * bh * sizeof(uint32_t));
   return w;
 }
 
@@ -533,10 +902,16 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   int32_t* slab = (int32_t*)(base + lay.slab_off);
   int2* changes = (int2*)(base + lay.changes_off);
   int32_t* nch = (int32_t*)(base + lay.nchanges_off);
+  uint16_t* e16 = (uint16_t*)(base + lay.e16_off);
+  int32_t* fb_list = (int32_t*)(base + lay.fb_off);
+  uint32_t* stats = (uint32_t*)(base + lay.stats_off);
+  int32_t* fb_count = (int32_t*)stats;  // head b at fb_count[b * kCounterStride]
+  uint32_t* err_max = stats + (size_t)kCounterStride * bh;
+  uint32_t* norm_max = err_max + bh;
   const int jpad_k = pad_to(kc, kAssignChunk), jpad_q = pad_to(qc, kAssignChunk);
   int rc = svoo_zero_f64(sums_k, (long long)bh * kc * 128, s);
   if (!rc) rc = svoo_zero_f64(sums_q, (long long)bh * qc * 128, s);
-  if (!rc) rc = svoo_zero_i32(nch, 2, s);
+  if (!rc) rc = svoo_zero_i32(nch, 2 * kCounterStride, s);
   // One side of an iteration: profiles of x's tokens live in the other side's centroid space.
   // The first iteration sorts the labels and sums every cluster; later ones list the tokens whose
   // label changed and move only their rows between the fp64 sums (the finalize resets the counter).
@@ -544,21 +919,32 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
                   int32_t* sorted_idx, int32_t* offsets, double* sums, int kx, int ko, int jpad, int32_t* cnt,
                   bool first) -> int {
     int r;
-    if ((r = prep_launch(cent, other, e_hi, e_lo, nullptr, bh, kx, ko, jpad, s))) return r;
+    // The certified fp16 pass needs the fp16 copy of E, which the fp64-MFMA prep writes (profile widths up
+    // to kPmMaxKp); wider profiles run the hi + lo kernel on every token.
+    const bool fp16 = ko <= kPmMaxKp;
+    if (fp16 && (r = svoo_zero_i32((int32_t*)stats, (long long)(kCounterStride + 2) * bh, s))) return r;
+    if ((r = prep_launch(cent, other, e_hi, e_lo, nullptr, bh, kx, ko, jpad, s, fp16 ? e16 : nullptr, err_max,
+                         norm_max)))
+      return r;
+    int2* chg = first ? nullptr : changes;
+    int32_t* nc = first ? nullptr : cnt;
+    r = fp16 ? assign16_launch(x, e16, e_hi, e_lo, err_max, norm_max, labels, bh, n, kx, jpad, fb_list, fb_count, s,
+                               chg, nc)
+             : assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s, chg, nc);
+    if (r) return r;
     if (first) {
-      if ((r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s))) return r;
       if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, slab, counts, nullptr, s)))
         return r;
       return svoo_centroid_update_impl(x, sorted_idx, slab, sizes, cent, cent, bh, n, kx, sums, s, 1);
     }
-    if ((r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s, changes, cnt))) return r;
     return svoo_centroid_delta_impl(x, changes, cnt, sums, sizes, cent, cent, bh, n, kx, cnt, s);
   };
   for (int it = 0; it < max_iters && rc == SVOO_OK; ++it) {
     if ((rc = side(k, k_cent, q_cent, k_labels, k_sizes, k_sorted_idx, k_offsets, sums_k, kc, qc, jpad_k, nch,
                    it == 0)))
       break;
-    if ((rc = side(q, q_cent, k_cent, q_labels, q_sizes, q_sorted_idx, q_offsets, sums_q, qc, kc, jpad_q, nch + 1,
+    if ((rc = side(q, q_cent, k_cent, q_labels, q_sizes, q_sorted_idx, q_offsets, sums_q, qc, kc, jpad_q,
+                   nch + kCounterStride,
                    it == 0)))
       break;
   }

@@ -161,6 +161,32 @@ def test_assign_matches_literal_argmin(gpu):
         assert diff.mean() < 1e-3
 
 
+
+@pytest.mark.parametrize("cfg_name,heads", [("C3", 4), ("C2", 3), ("C4", 2)])
+def test_certified_fp16_pass_equals_hi_lo_labels(gpu, cfg_name, heads):
+    """Inside svoo_co_cluster the assignment runs one fp16 MFMA pass and certifies a label when the best score
+    beats the second by more than twice a rigorous error bound; the other tokens go to the hi + lo kernel.
+    One iteration from seeded starts: the key labels equal the hi + lo kernel's (svoo_cocluster_assign) on the
+    initial centroids, and the query labels equal it in the space of the updated key centroids."""
+    from svoo_amd import synth
+    from svoo_amd.co_clustering import cocluster_assign, co_cluster_tokens_full
+
+    cfg = synth.CONFIGS[cfg_name]
+    say("certified fp16 pass vs hi+lo labels", cfg_name, heads)
+    q, k, _ = synth.make_qkv_device(cfg, gpu)
+    nv = cfg.video_tokens
+    q, k = q[0, :heads, :nv].contiguous(), k[0, :heads, :nv].contiguous()
+    qi = synth.init_indices(cfg, heads, cfg.num_q_centroids, nv, 1).to(gpu)
+    ki = synth.init_indices(cfg, heads, cfg.num_k_centroids, nv, 2).to(gpu)
+    r = co_cluster_tokens_full(q, k, cfg.num_q_centroids, cfg.num_k_centroids, 1, init_q_idx=qi, init_k_idx=ki)
+    qc0 = torch.gather(q, 1, qi[:, :, None].expand(-1, -1, 128))
+    kc0 = torch.gather(k, 1, ki[:, :, None].expand(-1, -1, 128))
+    klab = cocluster_assign(k, kc0, qc0)
+    qlab = cocluster_assign(q, qc0, r["kcentroids"])
+    torch.cuda.synchronize()
+    assert torch.equal(r["klabels"], klab)
+    assert torch.equal(r["qlabels"], qlab)
+
 def test_weighted_softmax_bit_exact(gpu):
     from svoo_amd.co_clustering import weighted_softmax
 
