@@ -21,7 +21,9 @@ constexpr int kCentBatch = 16;        // rows in flight per wave (double buffere
 __global__ void __launch_bounds__(256) centroid_accumulate_kernel(const uint32_t* __restrict__ x,
                                                                   const int32_t* __restrict__ sorted_idx,
                                                                   const int32_t* __restrict__ sorted_labels,
-                                                                  double* __restrict__ sums, int n, int k) {
+                                                                  double* __restrict__ sums, int n, int k,
+                                                                  const int32_t* __restrict__ guard, int limit) {
+  if (guard && *guard <= limit) return;
   // D = 128 fixed: a row is 64 uint32 words (bf16 pairs), one per lane.
   const int b = blockIdx.y;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -108,6 +110,15 @@ __global__ void zero_f64_kernel(double* __restrict__ p, long long n) {
   if (i < n) p[i] = 0.0;
 }
 
+// Grid-stride clear that runs only when *guard > limit (a cheap launch when it does not).
+constexpr int kGuardedZeroBlocks = 1024;
+__global__ void zero_f64_guarded_kernel(double* __restrict__ p, long long n, const int32_t* __restrict__ guard,
+                                        int limit) {
+  if (*guard <= limit) return;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+    p[i] = 0.0;
+}
+
 __global__ void zero_i32_kernel(int32_t* __restrict__ p, long long n) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
@@ -118,11 +129,12 @@ __global__ void __launch_bounds__(256) centroid_delta_kernel(const uint32_t* __r
                                                              const int2* __restrict__ changes,
                                                              const int32_t* __restrict__ nchanges,
                                                              double* __restrict__ sums, int32_t* __restrict__ sizes,
-                                                             int n, int k) {
+                                                             int n, int k, int limit) {
   const int lane = threadIdx.x % kWave;
   const int w0 = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
   const int nw = gridDim.x * (blockDim.x / kWave);
   const int total = *nchanges;
+  if (total > limit) return;  // the full recount handles this iteration
   for (int e = w0; e < total; e += nw) {
     const int2 c = changes[e];
     const int b = c.x / n, ol = c.y >> 16, nl = c.y & 0xffff;
@@ -157,20 +169,37 @@ int svoo_zero_i32(int32_t* p, long long n, hipStream_t stream) {
   return check_launch("zero_i32");
 }
 
+int svoo_zero_f64_guarded(double* p, long long n, const int32_t* guard, int limit, hipStream_t stream) {
+  if (n <= 0) return SVOO_OK;
+  hipLaunchKernelGGL(zero_f64_guarded_kernel, dim3(kGuardedZeroBlocks), dim3(256), 0, stream, p, n, guard, limit);
+  return check_launch("zero_f64_guarded");
+}
+
 // Moves the listed tokens between the (kept) fp64 sums and counts, then recomputes the centroids;
-// *reset (the list's counter) is cleared by the finalize.
+// *reset (the list's counter) is cleared by the finalize.  With more than `limit` listed tokens the delta
+// kernel does nothing: the caller has recounted every cluster instead (its guarded sort and sums).
 int svoo_centroid_delta_impl(const uint16_t* x, const int2* changes, const int32_t* nchanges, double* sums,
                              int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
-                             int32_t* reset, hipStream_t stream) {
+                             int32_t* reset, hipStream_t stream, int limit) {
   hipLaunchKernelGGL(centroid_delta_kernel, dim3(kDeltaBlocks), dim3(256), 0, stream, (const uint32_t*)x, changes,
-                     nchanges, sums, sizes, n, k);
+                     nchanges, sums, sizes, n, k, limit);
   const long long total = (long long)bh * k * 128;
   hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, sums,
                      sizes, old_c, new_c, total, 128, 1, reset);
   return check_launch("svoo_centroid_delta");
 }
 
-// sums must be zero on entry; it is zero again on return unless keep_sums.
+// sums must be zero on entry; it is zero again on return unless keep_sums.  With a guard the sums are
+// accumulated only when *guard > limit (the finalize is then the caller's).
+void svoo_centroid_accumulate_guarded(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
+                                      double* sums, int bh, int n, int k, const int32_t* guard, int limit,
+                                      hipStream_t stream) {
+  const int pos_per_block = 4 * kCentPosPerWave;
+  dim3 grid((n + pos_per_block - 1) / pos_per_block, bh);
+  hipLaunchKernelGGL(centroid_accumulate_kernel, grid, dim3(256), 0, stream, (const uint32_t*)x, sorted_idx,
+                     sorted_labels, sums, n, k, guard, limit);
+}
+
 int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
                               const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
                               double* sums, hipStream_t stream, int keep_sums) {
@@ -178,7 +207,7 @@ int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, cons
   const int pos_per_block = waves_per_block * kCentPosPerWave;
   dim3 grid((n + pos_per_block - 1) / pos_per_block, bh);
   hipLaunchKernelGGL(centroid_accumulate_kernel, grid, dim3(256), 0, stream, (const uint32_t*)x, sorted_idx,
-                     sorted_labels, sums, n, k);
+                     sorted_labels, sums, n, k, (const int32_t*)nullptr, 0);
   const long long total = (long long)bh * k * 128;
   hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, sums,
                      sizes, old_c, new_c, total, 128, keep_sums, (int32_t*)nullptr);

@@ -743,13 +743,17 @@ using namespace svoo;
 // Forward declarations of the other translation units' internal entry points.
 int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
                            int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
-                           hipStream_t stream);
+                           hipStream_t stream, const int32_t* guard = nullptr, int limit = 0);
+void svoo_centroid_accumulate_guarded(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
+                                      double* sums, int bh, int n, int k, const int32_t* guard, int limit,
+                                      hipStream_t stream);
+int svoo_zero_f64_guarded(double* p, long long n, const int32_t* guard, int limit, hipStream_t stream);
 int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
                               const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
                               double* sums, hipStream_t stream, int keep_sums = 0);
 int svoo_centroid_delta_impl(const uint16_t* x, const int2* changes, const int32_t* nchanges, double* sums,
                              int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
-                             int32_t* reset, hipStream_t stream);
+                             int32_t* reset, hipStream_t stream, int limit);
 int svoo_zero_i32(int32_t* p, long long n, hipStream_t stream);
 int svoo_zero_f64(double* p, long long n, hipStream_t stream);
 
@@ -908,13 +912,16 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   int32_t* fb_count = (int32_t*)stats;  // head b at fb_count[b * kCounterStride]
   uint32_t* err_max = stats + (size_t)kCounterStride * bh;
   uint32_t* norm_max = err_max + bh;
+  // changed tokens above which an iteration recounts every cluster instead of moving the changed ones
+  const int limit = (int)((long long)bh * n / 32);
   const int jpad_k = pad_to(kc, kAssignChunk), jpad_q = pad_to(qc, kAssignChunk);
   int rc = svoo_zero_f64(sums_k, (long long)bh * kc * 128, s);
   if (!rc) rc = svoo_zero_f64(sums_q, (long long)bh * qc * 128, s);
   if (!rc) rc = svoo_zero_i32(nch, 2 * kCounterStride, s);
   // One side of an iteration: profiles of x's tokens live in the other side's centroid space.
-  // The first iteration sorts the labels and sums every cluster; later ones list the tokens whose
-  // label changed and move only their rows between the fp64 sums (the finalize resets the counter).
+  // A full iteration sorts the labels and sums every cluster (sums zero on entry, kept on exit); an
+  // incremental one lists the tokens whose label changed and moves only their rows between the kept fp64
+  // sums (the finalize resets the counter).
   auto side = [&](const uint16_t* x, uint16_t* cent, const uint16_t* other, int32_t* labels, int32_t* sizes,
                   int32_t* sorted_idx, int32_t* offsets, double* sums, int kx, int ko, int jpad, int32_t* cnt,
                   bool first) -> int {
@@ -937,15 +944,26 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
         return r;
       return svoo_centroid_update_impl(x, sorted_idx, slab, sizes, cent, cent, bh, n, kx, sums, s, 1);
     }
-    return svoo_centroid_delta_impl(x, changes, cnt, sums, sizes, cent, cent, bh, n, kx, cnt, s);
+    // More changed tokens than `limit` (a share of all the tokens at which both updates take about the same
+    // time at the Wan shapes): recount every cluster from the sorted labels (guarded kernels, which return at
+    // once otherwise); else move the changed tokens.  The choice is made on the device from the count.
+    if ((r = svoo_zero_f64_guarded(sums, (long long)bh * kx * 128, cnt, limit, s))) return r;
+    if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, slab, counts, nullptr, s, cnt,
+                                    limit)))
+      return r;
+    svoo_centroid_accumulate_guarded(x, sorted_idx, slab, sums, bh, n, kx, cnt, limit, s);
+    return svoo_centroid_delta_impl(x, changes, cnt, sums, sizes, cent, cent, bh, n, kx, cnt, s, limit);
   };
+  // Iteration 1 recounts every cluster from the sorted labels.  Later iterations list the tokens whose label
+  // changed; with more than `limit` of them (after a random start, iteration 2 moves 30-90% of the tokens at the
+  // Wan2.1-14B 720p shape, which the per-token fp64 atomics of the incremental update handle ten times slower)
+  // the sorted recount runs instead, chosen on the device.
   for (int it = 0; it < max_iters && rc == SVOO_OK; ++it) {
     if ((rc = side(k, k_cent, q_cent, k_labels, k_sizes, k_sorted_idx, k_offsets, sums_k, kc, qc, jpad_k, nch,
                    it == 0)))
       break;
     if ((rc = side(q, q_cent, k_cent, q_labels, q_sizes, q_sorted_idx, q_offsets, sums_q, qc, kc, jpad_q,
-                   nch + kCounterStride,
-                   it == 0)))
+                   nch + kCounterStride, it == 0)))
       break;
   }
   // The stable sort of the final labels (the first iteration's sort already is when max_iters == 1).

@@ -19,7 +19,9 @@ constexpr int kMaxSortClusters = 16384;
 
 __global__ void __launch_bounds__(256) sort_hist_kernel(const int32_t* __restrict__ labels, int n, int k,
                                                         int nchunks, int32_t* __restrict__ counts,
-                                                        int32_t* __restrict__ err) {
+                                                        int32_t* __restrict__ err, const int32_t* __restrict__ guard,
+                                                        int limit) {
+  if (guard && *guard <= limit) return;
   extern __shared__ int32_t hist[];
   const int b = blockIdx.y, c = blockIdx.x;
   for (int i = threadIdx.x; i < k; i += blockDim.x) hist[i] = 0;
@@ -56,7 +58,9 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 // clusters per pass; every access of a chunk row is contiguous over the threads.
 __global__ void __launch_bounds__(kScanWaves * kWave) sort_scan_kernel(int32_t* __restrict__ counts, int k,
                                                                        int nchunks, int32_t* __restrict__ sizes,
-                                                                       int32_t* __restrict__ offsets) {
+                                                                       int32_t* __restrict__ offsets,
+                                                                       const int32_t* __restrict__ guard, int limit) {
+  if (guard && *guard <= limit) return;
   __shared__ int wsum[kScanWaves];
   const int b = blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   int32_t* cnt = counts + (size_t)b * k * nchunks;
@@ -97,7 +101,9 @@ __global__ void __launch_bounds__(kScanWaves * kWave) sort_scan_kernel(int32_t* 
 __global__ void __launch_bounds__(64) sort_scatter_kernel(const int32_t* __restrict__ labels, int n, int k,
                                                           int kbits, int nchunks, const int32_t* __restrict__ bases,
                                                           int32_t* __restrict__ sorted_idx,
-                                                          int32_t* __restrict__ sorted_labels) {
+                                                          int32_t* __restrict__ sorted_labels,
+                                                          const int32_t* __restrict__ guard, int limit) {
+  if (guard && *guard <= limit) return;
   extern __shared__ int32_t base[];
   const int b = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
   const int32_t* bs = bases + (size_t)b * k * nchunks;
@@ -146,19 +152,22 @@ extern "C" size_t svoo_cluster_sort_workspace_size(int bh, int n, int k) {
 }
 
 // Internal entry used by the co-clustering driver: the workspace pointer is already sized.
+// With a guard the three kernels do their work only when *guard > limit (a count on the device; the
+// co-clustering's choice between a full recount and the incremental update).
 int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
                            int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
-                           hipStream_t stream) {
+                           hipStream_t stream, const int32_t* guard, int limit) {
   const int nch = sort_nchunks(n);
   SVOO_REQUIRE((long long)k * nch < (1ll << 31), SVOO_ERR_UNSUPPORTED, "svoo_cluster_sort: k=%d x %d chunks too large",
                k, nch);
   hipLaunchKernelGGL(sort_hist_kernel, dim3(nch, bh), dim3(256), k * sizeof(int32_t), stream, labels, n, k, nch,
-                     counts, err);
+                     counts, err, guard, limit);
   int kbits = 0;
   while ((1 << kbits) < k) ++kbits;
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(bh), dim3(kScanWaves * kWave), 0, stream, counts, k, nch, sizes, offsets);
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(bh), dim3(kScanWaves * kWave), 0, stream, counts, k, nch, sizes, offsets,
+                     guard, limit);
   hipLaunchKernelGGL(sort_scatter_kernel, dim3(nch, bh), dim3(64), k * sizeof(int32_t), stream, labels, n, k, kbits,
-                     nch, counts, sorted_idx, sorted_labels);
+                     nch, counts, sorted_idx, sorted_labels, guard, limit);
   return check_launch("svoo_cluster_sort");
 }
 
@@ -175,5 +184,5 @@ extern "C" int svoo_cluster_sort(const int32_t* labels, int bh, int n, int k, in
   SVOO_REQUIRE(workspace && ws_bytes >= need, SVOO_ERR_WORKSPACE, "svoo_cluster_sort: workspace %zu < %zu",
                ws_bytes, need);
   return svoo_cluster_sort_impl(labels, bh, n, k, sorted_idx, sizes, offsets, sorted_labels, (int32_t*)workspace,
-                                nullptr, (hipStream_t)stream);
+                                nullptr, (hipStream_t)stream, nullptr, 0);
 }
