@@ -164,6 +164,13 @@ static inline size_t pm_smem(int kp) {
   return pm_praw_bytes(kp) + kPmRows * sizeof(double) + (size_t)kPmChunk * kPmChunkStride * sizeof(uint16_t);
 }
 
+// Element offset of E16[row][col] within a head: 32-row tiles of 8 KB, each [k-step 0..7][lane 0..63][8],
+// where lane 32 hh + r holds columns 16 ks + 8 hh .. + 7 of tile row r.  The A operand of one k-step of
+// v_mfma_f32_32x32x16_f16 is then 1 KB of consecutive bytes, lane i at 16 i.
+__host__ __device__ __forceinline__ size_t e16_offset(int row, int col) {
+  return (size_t)(row >> 5) * 4096 + (col >> 4) * 512 + (((col >> 3) & 1) * 32 + (row & 31)) * 8 + (col & 7);
+}
+
 __device__ __forceinline__ double bf16_half_f64(uint32_t w, int hi) {
   return (double)bf16_to_f32((uint16_t)(hi ? (w >> 16) : (w & 0xffffu)));
 }
@@ -297,7 +304,7 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
         const double err = es - (double)(float)h16;  // exact
         err2[v] += (float)(err * err);
         nrm2[v] += (float)((double)(float)h16 * (double)(float)h16);
-        e16[((size_t)bidx * jpad + row) * 128 + dd] = __builtin_bit_cast(uint16_t, h16);
+        e16[(size_t)bidx * jpad * 128 + e16_offset(row, dd)] = __builtin_bit_cast(uint16_t, h16);
       }
     }
   }
@@ -525,10 +532,19 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 //   * The label is certified when the best score exceeds the second by more than 2 B: then it is the
 //     exact argmax of x . E (no tie is possible).  Other tokens (near-equal top scores, a zero token) go
 //     to the head's fallback list for the hi + lo kernel, which also applies its tie rule.
-// Each lane keeps the top two tagged scores of its cluster rows (median-of-three update) and the tile of
-// the best.  Padding rows (j .. jpad-1) are zero in E16, so they score exactly 0: as the runner-up such a
+// Each lane keeps the top two tagged scores of its cluster rows (updated two scores at a time) and the tile
+// of the best.  Padding rows (j .. jpad-1) are zero in E16, so they score exactly 0: as the runner-up such a
 // row only tightens the test, and a token whose best row is padding goes to the fallback.
+// E16 is stored in MFMA operand order (e16_offset) and streams through LDS in 16 KB chunks by LDS DMA
+// issued from inline assembly; measured with per-wave cycle stamps at C3's key side, the main loop runs at
+// the MFMA rate of two waves per SIMD (about 61 cycles per 32-cycle MFMA and wave), and the token
+// conversion before it and the certification after it take a quarter of a block's time.
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+// Through a by-value parameter: this compiler's __builtin_bit_cast of a vector element operand (v[e], v.y)
+// reads element 0 whatever the index.
+__device__ __forceinline__ f16x2_t as_f16x2(uint32_t w) { return __builtin_bit_cast(f16x2_t, w); }
 __device__ __forceinline__ f16x8_t as_f16x8(u32x4_t v) { return __builtin_bit_cast(f16x8_t, v); }
 __device__ __forceinline__ f32x16_t mfma32x32x16_f16(f16x8_t a, f16x8_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -540,39 +556,51 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
                           int32_t* __restrict__ labels, int n, int j, int jpad, int2* __restrict__ changes,
                           int32_t* __restrict__ nchanges, int32_t* __restrict__ fb_list,
                           int32_t* __restrict__ fb_count) {
-  __shared__ __attribute__((aligned(16))) uint16_t s_e[2][kAssignChunk * 128];
+  // two chunk buffers of 16 KB, each two 32-row tiles in the layout of e16_offset
+  __shared__ __attribute__((aligned(16))) uint16_t s_e[2 * kAssignChunk * 128];
   const int bidx = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int h = lane / 32, l32 = lane % 32;
   const int tok0 = blockIdx.x * kAsgTok + wave * kAsgTokWave;
   const uint16_t* xb = x + (size_t)bidx * n * 128;
-  const uint16_t* eb = e16 + (size_t)bidx * jpad * 128;
+  const char* eb = (const char*)(e16 + (size_t)bidx * jpad * 128);
   const int nchunks = jpad / kAssignChunk;
 
-  const int prow = lane / 16, pch = lane % 16;
+  // A chunk is 16 KB contiguous in e16 and in LDS: wave w copies bytes [4 KB w, 4 KB w + 4 KB), 1 KB per
+  // instruction (inline-assembly DMA, waited for before each chunk's barrier).
+  const uint32_t voff = wave * 4096 + lane * 16;
+  const uint32_t lds0 = lds_addr(s_e) + wave * 4096;
   auto issue = [&](int c, int bf) __attribute__((always_inline)) {
+    const char* src = eb + (size_t)c * (kAssignChunk * 256);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int r = 16 * wave + 4 * g + prow;
-      lds_dma16(eb + (size_t)(c * kAssignChunk + r) * 128 + swz(r, pch) * 8, &s_e[bf][(16 * wave + 4 * g) * 128]);
-    }
+    for (int g = 0; g < 4; ++g) lds_dma16_asm(src, voff + g * 1024, lds0 + bf * (kAssignChunk * 256) + g * 1024);
   };
   issue(0, 0);
 
-  // Tokens: fp16, scaled per token.
+  // Tokens: fp16, scaled per token.  The previous labels, compared at the end when the changes are listed,
+  // are loaded here so that their latency is spent under the pass.
+  int prevl[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int tok = tok0 + cb * 32 + l32;
+    prevl[cb] = (nchanges && h == 0 && tok < n) ? labels[(size_t)bidx * n + tok] : -1;
+  }
   u32x4_t xop[4][8];
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
     const int row = min(tok0 + cb * 32 + l32, n - 1);
     const u32x4_t* src = (const u32x4_t*)(xb + (size_t)row * 128);
     u32x4_t raw[8];
-    uint32_t mbits = 0;
+    // largest magnitude bits of the lane's 64 components, two halves at a time (packed 16-bit max)
+    u16x2_t m2 = {0, 0};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       raw[ks] = src[ks * 2 + h];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) mbits = max(mbits, max(raw[ks][e] & 0x7fffu, (raw[ks][e] >> 16) & 0x7fffu));
+      for (int e = 0; e < 4; ++e) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2_t, raw[ks][e] & 0x7fff7fffu));
     }
+    uint32_t mbits = max((uint32_t)m2[0], (uint32_t)m2[1]);
     mbits = max(mbits, (uint32_t)__shfl_xor((int)mbits, 32));
     // biased exponent of the largest component (subnormals count as exponent -126)
     const int be = max(1, (int)(mbits >> 7));
@@ -586,9 +614,9 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
         xop[cb][ks][e] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
       }
   }
-  const int sw = swz(l32, 0), g = sw >> 1;
-  const int abase = l32 * 128 + 8 * (h ^ (sw & 1));
-#define AOFF(ks) (abase + 16 * ((ks) ^ g))
+  // A operand of k-step ks of a tile: 16 bytes per lane at tile + 1 KB ks + 16 lane (immediate offsets)
+  const uint16_t* alane = s_e + lane * 8;
+#define AOFF(ks) ((ks) * 512)
 
   float top1[4], top2[4];
   int tbase[4];
@@ -608,39 +636,42 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   auto epi = [&](int cb, int jb) __attribute__((always_inline)) {
     const float prev = top1[cb];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float t = __uint_as_float((__float_as_uint(acc[cb][r]) & ~15u) | (uint32_t)(15 - r));
-      top2[cb] = __builtin_amdgcn_fmed3f(top1[cb], top2[cb], t);
-      top1[cb] = __builtin_amdgcn_fmed3f(top1[cb], t, pinf);
+    for (int r = 0; r < 16; r += 2) {
+      const float ta = __uint_as_float((__float_as_uint(acc[cb][r]) & ~15u) | (uint32_t)(15 - r));
+      const float tb = __uint_as_float((__float_as_uint(acc[cb][r + 1]) & ~15u) | (uint32_t)(14 - r));
+      const float mid = __builtin_amdgcn_fmed3f(top1[cb], ta, tb);
+      top1[cb] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(top1[cb], ta), tb);
+      top2[cb] = __builtin_elementwise_maximum(top2[cb], mid);
     }
     tbase[cb] = top1[cb] != prev ? jb : tbase[cb];
   };
   // Two token blocks' MFMAs, their accumulator chains interleaved (a chain's next MFMA waits on the previous),
   // with the A operands (E16 rows of the 32-row tile) read from LDS two k-steps ahead into a ring of three.
   auto mfmas2 = [&](int cb0, const uint16_t* tile) __attribute__((always_inline)) {
-    u32x4_t ring[3];
+    u32x4_t ring[4];
     ring[0] = *(const u32x4_t*)(tile + AOFF(0));
     ring[1] = *(const u32x4_t*)(tile + AOFF(1));
+    ring[2] = *(const u32x4_t*)(tile + AOFF(2));
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      acc[cb0] = mfma32x32x16_f16(as_f16x8(ring[ks % 3]), as_f16x8(xop[cb0][ks]), ks ? acc[cb0] : f32x16_t{});
-      if (ks + 2 < 8) ring[(ks + 2) % 3] = *(const u32x4_t*)(tile + AOFF(ks + 2));
+      acc[cb0] = mfma32x32x16_f16(as_f16x8(ring[ks % 4]), as_f16x8(xop[cb0][ks]), ks ? acc[cb0] : f32x16_t{});
+      if (ks + 3 < 8) ring[(ks + 3) % 4] = *(const u32x4_t*)(tile + AOFF(ks + 3));
       acc[cb0 + 1] =
-          mfma32x32x16_f16(as_f16x8(ring[ks % 3]), as_f16x8(xop[cb0 + 1][ks]), ks ? acc[cb0 + 1] : f32x16_t{});
+          mfma32x32x16_f16(as_f16x8(ring[ks % 4]), as_f16x8(xop[cb0 + 1][ks]), ks ? acc[cb0 + 1] : f32x16_t{});
     }
   };
   // Software pipeline within the wave: the MFMAs of blocks {0, 1} run while the VALU updates the top two of
   // blocks {2, 3} of the previous 32-row tile, then the MFMAs of {2, 3} beside the updates of {0, 1}; per k-step
   // an MFMA, six VALU instructions, the LDS read two k-steps ahead, an MFMA, six VALU instructions.
   auto interleave = [&]() __attribute__((always_inline)) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-      if (i + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      if (i + 3 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
     }
   };
   // Before the first tile the pending updates of blocks 2 and 3 see scores of -FLT_MAX, below every real score
@@ -655,8 +686,9 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   for (int c = 0; c < nchunks; ++c) {
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (c + 1 < nchunks) issue(c + 1, (c + 1) & 1);
-    const uint16_t* se = s_e[c & 1];
+    // The last step copies the last chunk again into the free buffer: no branch around the copy.
+    issue(min(c + 1, nchunks - 1), (c + 1) & 1);
+    const uint16_t* se = alane + (c & 1) * (kAssignChunk * 128);
 #pragma unroll
     for (int rb = 0; rb < kAssignChunk / 32; ++rb) {
       const uint16_t* tile = se + rb * 32 * 128;
@@ -678,6 +710,7 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   epi(2, pend_jb);
   epi(3, pend_jb);
 #undef AOFF
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the extra copy lands before the block ends
   const float dd = __uint_as_float(err_max[bidx]), em = __uint_as_float(norm_max[bidx]);
   const float slack = dd + 0x1p-15f * em;
   int lab[4], oldl[4];
@@ -686,15 +719,15 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   int nfb = 0, nch_wave = 0;
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
-    // |x~| of the fp16 operands themselves (fp32 sum of 128 exact squares; 1.001 below covers its rounding)
+    // |x~| of the fp16 operands themselves: fp32 sums of exact fp16 squares, two per v_dot2_f32_f16 (at most
+    // two roundings per step over 64 steps; 1.001 below covers them)
     float n2 = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const auto hv = __builtin_bit_cast(_Float16 __attribute__((ext_vector_type(2))), xop[cb][ks][e]);
-        const float lo = (float)hv[0], hi = (float)hv[1];
-        n2 = fmaf(lo, lo, fmaf(hi, hi, n2));
+        const f16x2_t hv = as_f16x2(xop[cb][ks][e]);
+        n2 = __builtin_amdgcn_fdot2(hv, hv, n2, false);
       }
     n2 += __shfl_xor(n2, 32);
     const float xnorm = sqrtf(n2);
@@ -714,13 +747,33 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
     minev[cb] = h == 0 && tok < n;
     fbm[cb] = __ballot(minev[cb] && !certv[cb]);
     // labels holds the previous iteration's labels when the changes are listed
-    oldl[cb] = (minev[cb] && certv[cb] && nchanges) ? labels[(size_t)bidx * n + tok] : lab[cb];
+    oldl[cb] = (minev[cb] && certv[cb] && nchanges) ? prevl[cb] : lab[cb];
     chm[cb] = __ballot(minev[cb] && certv[cb] && oldl[cb] != lab[cb]);
     nfb += (int)__popcll(fbm[cb]);
     nch_wave += (int)__popcll(chm[cb]);
   }
-  const int fbase = wave_reserve(fb_count + (size_t)bidx * kCounterStride, nfb);
-  const int cbase = nchanges ? wave_reserve(nchanges, nch_wave) : 0;
+  // One reservation per block and list: the four waves' counts meet in LDS, lane 0 of wave 0 reserves the
+  // fallback slots and lane 0 of wave 1 the change slots (side by side), and each wave takes its share in
+  // wave order.  Tens of thousands of per-wave atomics on the one change counter serialise in the L2.
+  __shared__ int s_cnt[2][4], s_base[2];
+  if (lane == 0) {
+    s_cnt[0][wave] = nfb;
+    s_cnt[1][wave] = nch_wave;
+  }
+  __syncthreads();
+  if (lane == 0 && wave < 2) {
+    const int tot = s_cnt[wave][0] + s_cnt[wave][1] + s_cnt[wave][2] + s_cnt[wave][3];
+    int base = 0;
+    if (tot > 0 && wave == 0) base = atomicAdd(fb_count + (size_t)bidx * kCounterStride, tot);
+    if (tot > 0 && wave == 1 && nchanges) base = atomicAdd(nchanges, tot);
+    s_base[wave] = base;
+  }
+  __syncthreads();
+  int fbase = s_base[0], cbase = s_base[1];
+  for (int w = 0; w < wave; ++w) {
+    fbase += s_cnt[0][w];
+    cbase += s_cnt[1][w];
+  }
   int fpre = 0, cpre = 0;
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {

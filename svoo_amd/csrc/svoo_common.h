@@ -87,6 +87,20 @@ __device__ __forceinline__ void lds_dma16(const void* src, uint16_t* lds_base) {
                                    (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
+// The same copy issued from inline assembly: 16 bytes per lane from sbase + voff (bytes) to LDS byte address
+// lds + 16 * lane (sbase and lds wave-uniform).  The compiler neither sees nor counts it, so its waits for the
+// kernel's own LDS reads stay exact (it treats a visible LDS DMA as an LDS event that may complete out of
+// order and answers every later LDS read with lgkmcnt(0)).  The caller waits for completion explicitly
+// (s_waitcnt vmcnt) before the barrier that publishes the data.  M0 needs one wait state after its write.
+__device__ __forceinline__ void lds_dma16_asm(const void* sbase, uint32_t voff, uint32_t lds) {
+  __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+                   : "memory", "m0");
+}
+// LDS byte address of a __shared__ object, wave-uniform.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+
 // Max / sum of a value and its partner lane (lane ^ 32), in both lanes: one v_permlane32_swap (a VALU
 // op) instead of a ds_bpermute round trip through LDS.  The swap returns {lanes 0-31 of the first operand
 // with lanes 0-31 of the second in the upper half, lanes 32-63 of the first in the lower half with lanes

@@ -162,20 +162,29 @@ def test_assign_matches_literal_argmin(gpu):
 
 
 
-@pytest.mark.parametrize("cfg_name,heads", [("C3", 4), ("C2", 3), ("C4", 2)])
-def test_certified_fp16_pass_equals_hi_lo_labels(gpu, cfg_name, heads):
+@pytest.mark.parametrize("cfg_name,heads,zero01", [("C3", 4, False), ("C2", 3, False), ("C4", 2, False),
+                                                   ("C2", 3, True)])
+def test_certified_fp16_pass_equals_hi_lo_labels(gpu, cfg_name, heads, zero01):
     """Inside svoo_co_cluster the assignment runs one fp16 MFMA pass and certifies a label when the best score
     beats the second by more than twice a rigorous error bound; the other tokens go to the hi + lo kernel.
     One iteration from seeded starts: the key labels equal the hi + lo kernel's (svoo_cocluster_assign) on the
-    initial centroids, and the query labels equal it in the space of the updated key centroids."""
+    initial centroids, and the query labels equal it in the space of the updated key centroids.
+
+    With zero01 the token components d = 0, 1 (mod 8) are zero: the bound scales with the token norm, and a
+    norm taken from those components alone (the first 32-bit word of each 16-byte operand) is zero, which
+    certifies every near-tie the fp16 rounding can flip."""
     from svoo_amd import synth
     from svoo_amd.co_clustering import cocluster_assign, co_cluster_tokens_full
 
     cfg = synth.CONFIGS[cfg_name]
-    say("certified fp16 pass vs hi+lo labels", cfg_name, heads)
+    say("certified fp16 pass vs hi+lo labels", cfg_name, heads, "zero d%8 in {0,1}" if zero01 else "")
     q, k, _ = synth.make_qkv_device(cfg, gpu)
     nv = cfg.video_tokens
     q, k = q[0, :heads, :nv].contiguous(), k[0, :heads, :nv].contiguous()
+    if zero01:
+        dims = torch.arange(128, device=gpu)
+        keep = ((dims % 8) >= 2).to(q.dtype)
+        q, k = (q * keep).contiguous(), (k * keep).contiguous()
     qi = synth.init_indices(cfg, heads, cfg.num_q_centroids, nv, 1).to(gpu)
     ki = synth.init_indices(cfg, heads, cfg.num_k_centroids, nv, 2).to(gpu)
     r = co_cluster_tokens_full(q, k, cfg.num_q_centroids, cfg.num_k_centroids, 1, init_q_idx=qi, init_k_idx=ki)
