@@ -57,7 +57,8 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-kernel-table", action="store_true",
                     help="skip the per-kernel table (one extra call under torch.profiler)")
-    ap.add_argument("--cpu-heads", type=int, default=1, help="heads in the CPU baseline sample")
+    ap.add_argument("--cpu-heads", type=int, default=2,
+                    help="heads in the CPU baseline sample (a fixed subset spread over the heads)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "vbsa_attn_C3_traffic.json"),
                     help="measured HBM traffic of the attention kernel (from rocprofv3 --pmc), if present")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -792,45 +793,59 @@ def cpu_baseline_dit(model, lat, txt, rho, top_p, dmin, dmax, nheads, t_step_ms,
     }
 
 
+CPU_BUDGET_S = 30.0  # the CPU sample repeats (up to 3 runs, median) while its total stays in this budget
+
+
 def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms, hunyuan=False, ear=False):
-    """The numpy oracle on ``nheads`` heads of the same inputs; latency scaled linearly to all heads."""
+    """The numpy oracle on a fixed subset of ``nheads`` heads of the same inputs (heads spread evenly: 0 and H/2
+    for two), timed up to 3 times within CPU_BUDGET_S (median); latency scaled linearly to all heads."""
     import numpy as np
 
     from oracle import svoo_oracle as O
 
     h, n, d = cfg.heads, cfg.tokens, cfg.head_dim
-    sel = list(range(nheads))
+    nheads = max(1, min(nheads, h))
+    sel = sorted({(i * h) // nheads for i in range(nheads)})
+    nheads = len(sel)
     f = lambda t: t[:, sel].float().cpu().numpy()  # noqa: E731
     qn, kn, vn = f(q), f(k), f(v)
     qi = q_init.view(h, -1, d)[sel].float().cpu().numpy()
     ki = k_init.view(h, -1, d)[sel].float().cpu().numpy()
     rs = [ratios[i] for i in sel]
-    t0 = time.perf_counter()
-    if hunyuan:
-        O.hunyuan_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
-                                 cfg.text_tokens, cfg.text_tokens, init_q_centroids=qi, init_k_centroids=ki,
-                                 attn_dtype=np.float32)
-    elif ear:
-        O.ear_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs, 1.0,
-                             init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
-    else:
-        O.svoo_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
-                              init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
-    t = time.perf_counter() - t0
+
+    def one_run():
+        t0 = time.perf_counter()
+        if hunyuan:
+            O.hunyuan_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p,
+                                     rs, cfg.text_tokens, cfg.text_tokens, init_q_centroids=qi, init_k_centroids=ki,
+                                     attn_dtype=np.float32)
+        elif ear:
+            O.ear_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
+                                 1.0, init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
+        else:
+            O.svoo_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
+                                  init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
+        return time.perf_counter() - t0
+
+    runs = [one_run()]
+    while len(runs) < 3 and sum(runs) + runs[0] <= CPU_BUDGET_S:
+        runs.append(one_run())
+    t = float(np.median(runs))
     per_head = t / nheads
     call_s = per_head * h
-    log(f"CPU oracle: {t:.2f}s for {nheads} head(s) -> {call_s:.1f}s per {h}-head call")
+    log(f"CPU oracle: {[round(x, 2) for x in runs]} s for heads {sel} -> {call_s:.1f}s per {h}-head call")
     return {
         "value": round(4.0 * nheads * float(n) ** 2 * d / t / 1e12, 5),
         "unit": "TFLOP/s (dense-equivalent)",
         "cores": cpu_threads(),
         "kind": "port",
-        "sample": f"{nheads} of {h} heads of the same inputs, full call (k-means {cfg.kmeans_iters} warm-started "
+        "sample": f"heads {sel} of {h} of the same inputs, full call (k-means {cfg.kmeans_iters} warm-started "
                   f"iterations, {'EAR scoring and selection' if ear else 'mask'}, permutes, fp32 "
-                  f"{'compensated ' if ear else ''}block-sparse attention) in the numpy oracle: {t:.2f} s; "
-                  f"scaled x{h / nheads:g} to {call_s:.1f} s per call = {call_s * 1e3 / t_call_ms:.0f}x the GPU "
-                  f"latency",
+                  f"{'compensated ' if ear else ''}block-sparse attention) in the numpy oracle: median of "
+                  f"{len(runs)} run(s) {t:.2f} s; scaled x{h / nheads:g} to {call_s:.1f} s per call = "
+                  f"{call_s * 1e3 / t_call_ms:.0f}x the GPU latency",
         "call_s_scaled": round(call_s, 3),
+        "runs_s": [round(x, 3) for x in runs],
     }
 
 

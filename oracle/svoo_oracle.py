@@ -12,8 +12,12 @@ Rounding contract (applies to the GPU implementation as well)
 * Dot products of stored (bf16 or fp32) values are evaluated exactly (float64
   sums of exactly representable products) and rounded to float32, then to the
   storage dtype, where the reference rounds a matmul output.
-* Centroid sums are exact (float64), rounded to float32, divided by the count in
-  float32 (IEEE division) and rounded to the storage dtype.
+* Centroid sums are float64, rounded to float32, divided by the count in
+  float32 (IEEE division) and rounded to the storage dtype.  A float64 sum of
+  bf16 values is exact while, per cluster and dimension, the members' exponent
+  span plus log2(member count) stays within 45 bits (53-bit significand minus
+  bf16's 8; about 28 binades at N = 75600); beyond that it rounds, and sums
+  taken in another order can differ in the last float64 bits.
 * Sorting is stable: ties go to the lower original index (-0.0 and +0.0 tie).
 * EAR (error-aware routing): value centroids are the exact member sum rounded to
   bf16, divided by the bf16-rounded count (the reference's bf16 tensor ops); the
@@ -176,8 +180,9 @@ def centroid_update(x, labels, old_centroids, dtype: str = "bf16") -> Tuple[np.n
 
     Follows ``svoo/co_clustering.py:253-303`` (``triton_centroid_update_sorted_euclid``):
     ``sums / max(count, 1)`` in float32, ``torch.where(count == 0, old, mean)``,
-    cast to the token dtype.  Contract: the member sum is exact (float64 of
-    bf16/fp32 values), rounded to float32, then divided by ``float32(count)``.
+    cast to the token dtype.  Contract: the member sum is taken in float64 (exact
+    under the exponent-span condition of the module docstring), rounded to float32,
+    then divided by ``float32(count)``.
     """
     x = np.asarray(x)
     labels = np.asarray(labels).astype(np.int64)

@@ -3,14 +3,18 @@
 // accumulate: each wave owns 128 consecutive sorted positions.  Labels are non-decreasing along
 //   sorted positions, so the wave walks its rows in order, keeping two fp64 partial sums per lane
 //   (lane l owns dims 2l, 2l+1 of a 128-dim row) and flushing them with one fp64 atomicAdd per
-//   lane whenever the label changes.  Sums of bf16 values are exact in fp64, so the result does
-//   not depend on the order of the atomics.  The wave's indices and labels arrive in two vector
-//   loads; rows are then fetched 16 at a time, one batch ahead of the accumulation.
+//   lane whenever the label changes.  A sum of bf16 values is exact in fp64 while, per cluster and
+//   dimension, the members' exponent span (largest exponent minus smallest nonzero one) plus
+//   log2(member count) stays within 53 - 8 = 45 bits (about 28 binades at N = 75600); then the result
+//   does not depend on the order of the atomics.  Beyond that the fp64 sums round and the last bits can
+//   depend on that order.  The wave's indices and labels arrive in two vector loads; rows are then
+//   fetched 16 at a time, one batch ahead of the accumulation.
 // finalize: centroid = bf16(f32(sum) / f32(size)), size 0 keeps the old centroid; the sum buffer
 //   is cleared on the way out so the next update starts from zero (or kept, for the delta update).
 // delta: the co-clustering's later iterations move only the rows whose label changed: one wave per
 //   listed token subtracts its row from the old cluster's sums and adds it to the new one's (fp64
-//   atomics; exact, so the sums equal a full recount) and moves one count.
+//   atomics) and moves one count.  Under the exponent-span condition above every partial sum is exact,
+//   so the sums equal a full recount bit for bit; beyond it they can differ in the last fp64 bits.
 #include "svoo_common.h"
 
 namespace svoo {

@@ -5,13 +5,19 @@
 // argmax_j x . E_j with E = P C ([J x D]).  That turns the assignment into one [N x D] x [D x J]
 // GEMM with an argmax epilogue, instead of recomputing x C^T for every tile of J.
 //
-// prep:   P = l2norm(bf16(A B^T)) with exact (fp64) dots, E = P B in fp64, split into two bf16
-//         matrices E_hi + E_lo so the bf16 MFMA sees E to ~16 significant bits.
-// assign: 4 waves x 128 tokens per block; token rows stay in registers as the MFMA B operand,
-//         E streams through LDS in 64-row chunks (hi and lo, double buffered, LDS DMA), and each
-//         lane keeps a running argmax over the 16 cluster rows it holds of every 32x32 tile.
-//         From the second iteration on it also lists the tokens whose label changed, and the
-//         centroid sums are updated from that list alone (exact fp64, so equal to a full recount).
+// prep:   P = l2norm(bf16(A B^T)) with exact (fp64) dots, E = P B, written as two bf16 matrices
+//         E_hi + E_lo (the bf16 MFMA then sees E to ~16 significant bits) and as a scaled fp16 copy E16
+//         with the per-head error maxima of that copy.
+// assign16: one fp16 MFMA pass over E16 with a rigorous score-error bound; a token whose best score
+//         beats the second by more than twice the bound has the exact argmax label, the others go to a
+//         per-head list.
+// assign: 4 waves x 128 tokens per block (all tokens, or the listed ones); token rows stay in registers
+//         as the MFMA B operand, E_hi and E_lo stream through LDS in 64-row chunks (double buffered,
+//         LDS DMA), and each lane keeps a running argmax over the 16 cluster rows it holds of every 32x32
+//         tile.
+// From the second iteration on the passes list the tokens whose label changed, and the centroid sums
+// are updated from that list alone (fp64; equal to a full recount while the sums are exact, see
+// centroid.hip), or recounted when many labels changed.
 #include "svoo_common.h"
 
 namespace svoo {
