@@ -36,6 +36,36 @@ from .permute import apply_inverse_permutation, apply_inverse_permutation_bshd, 
 from . import _lib
 
 
+def _env_on(name: str) -> bool:
+    """Truthiness of a diagnostic switch as the reference reads ``SVG_REUSE_DEBUG``: anything but unset, ``0``,
+    empty, ``false`` or ``False``."""
+    return os.getenv(name, "0") not in ("0", "", "false", "False")
+
+
+def save_qk(query, key, timestep, layer_idx) -> Optional[str]:
+    """Activation capture of the self-attention inputs (``svoo/models/wan/attention.py:217-240``).
+
+    With ``SAVE_QK=1``, a ``timestep`` (the scheduler's value, ``timestep[0]`` of a tensor) at or above
+    ``SAVE_QK_START_STEP`` (default 0) and ``SAVE_QK_DIR`` set, writes ``{dir}/step{timestep}/layer{layer_idx}.pt``
+    holding ``{"q", "k"}`` (host copies of the ``[B, H, S, D]`` tensors after norm and RoPE), ``"timestep"`` and
+    ``"layer_idx"``.  Returns the file written, or None.
+    """
+    if os.getenv("SAVE_QK", "0") != "1" or timestep is None:
+        return None
+    if isinstance(timestep, torch.Tensor):
+        step = timestep[0].item() if timestep.dim() > 0 else timestep.item()
+    else:
+        step = timestep
+    save_dir = os.getenv("SAVE_QK_DIR", "")
+    if step < int(os.getenv("SAVE_QK_START_STEP", "0")) or not save_dir:
+        return None
+    step_dir = os.path.join(save_dir, f"step{step}")
+    os.makedirs(step_dir, exist_ok=True)
+    path = os.path.join(step_dir, f"layer{layer_idx}.pt")
+    torch.save({"q": query.detach().cpu(), "k": key.detach().cpu(), "timestep": step, "layer_idx": layer_idx}, path)
+    return path
+
+
 def _permute_rows(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
     b, h, s, d = x.shape
     inp = x.reshape(b * h, s, d).contiguous()
@@ -201,6 +231,7 @@ class WanAttn_SAPAttn_Processor:
                                                                is_causal=False)
             hidden_states_img = hidden_states_img.transpose(1, 2).flatten(2, 3).type_as(query)
 
+        save_qk(query, key, timestep, self.layer_idx)
         if timestep is None:
             hidden_states = F.scaled_dot_product_attention(query, key, value, attn_mask=attention_mask,
                                                            dropout_p=0.0, is_causal=False)
@@ -292,20 +323,35 @@ class WanAttn_SAPAttn_Processor:
         self._check_variant()
         return self._co_cluster(query, key, self.kmeans_iter_step, warm=self.kmeans_warm_start)
 
-    def should_recluster(self) -> bool:
-        """Reuse schedule of ``svoo/models/wan/attention.py:682-711``."""
+    def should_recluster(self, trace: bool = False) -> bool:
+        """Reuse schedule of ``svoo/models/wan/attention.py:682-711``.  With ``trace`` and ``SVG_REUSE_DEBUG`` set,
+        prints the reference's ``[reuse]`` lines (the offset is None before ``start_reuse_step``, and an interval
+        below 1 counts as 1, as in ``svoo/models/hunyuan10/attention.py:851-884``)."""
+        debug = trace and _env_on("SVG_REUSE_DEBUG")
         step = self.current_inference_step
         recluster = True
+        if debug:
+            print(f"[reuse] current_step={step}, start_reuse_step={self.start_reuse_step}, "
+                  f"reuse_interval={self.reuse_interval}")
         if step is not None and self.start_reuse_step is not None and self.start_reuse_step > 0:
+            offset = None
             if step >= self.start_reuse_step:
-                recluster = (step - self.start_reuse_step) % self.reuse_interval == 0
-        if not recluster and self._cached_clustering_results is None:
-            recluster = True
+                offset = step - self.start_reuse_step
+                recluster = offset % max(1, int(self.reuse_interval)) == 0
+            if debug:
+                print(f"[reuse] offset={offset}, should_recluster={recluster}")
+        if not recluster:
+            if self._cached_clustering_results is None:
+                if debug:
+                    print("[reuse] No cached clustering results, forcing recluster")
+                recluster = True
+            elif debug:
+                print("[reuse] Reusing cached clustering results")
         return recluster
 
     def kmeans_clustering(self, query, key, layer_idx):
         """Co-cluster (or return the cached clustering) and refresh the reuse cache (``:669-863``)."""
-        if not self.should_recluster():
+        if not self.should_recluster(trace=True):
             return self._cached_clustering_results
         if not self.centroids_init:
             r = self.kmeans_init(query, key, layer_idx)
@@ -313,7 +359,42 @@ class WanAttn_SAPAttn_Processor:
         else:
             r = self.kmeans_step(query, key, layer_idx)
         self._cached_clustering_results = r
+        if os.getenv("COMPUTE_REUSE_SIMILARITY", "0") == "1":
+            self.report_reuse_similarity(r, layer_idx, query.size(1))
         return r
+
+    def report_reuse_similarity(self, r, layer_idx, num_heads):
+        """Label agreement between this clustering and the previous one of the same (layer, head)
+        (``svoo/models/wan/attention.py:821-861``): the normalised mutual information (arithmetic mean) of the
+        query labels and of the key labels of the first batch element, printed as ``[Reuse Similarity]`` lines
+        and returned as ``{head: (prev_step, q_nmi, k_nmi)}``.  Needs scikit-learn (skipped without it, as in the
+        reference)."""
+        step = self.current_inference_step
+        out = {}
+        if step is None:
+            return out
+        hist = self.__dict__.setdefault("_clustering_history", {})
+        ql, kl = r["qlabels"], r["klabels"]
+        if ql.dim() != 2 or kl.dim() != 2 or ql.size(0) // num_heads < 1:
+            return out
+        try:
+            from sklearn.metrics import normalized_mutual_info_score
+        except ImportError:
+            normalized_mutual_info_score = None
+        for h in range(num_heads):
+            q_now, k_now = ql[h].cpu().clone(), kl[h].cpu().clone()
+            key_ = (layer_idx, h)
+            prev = [st for st in hist.get(key_, {}) if st < step]
+            if step > 0 and prev and normalized_mutual_info_score is not None:
+                ps = max(prev)
+                pq, pk = hist[key_][ps]
+                q_nmi = normalized_mutual_info_score(pq.numpy(), q_now.numpy(), average_method="arithmetic")
+                k_nmi = normalized_mutual_info_score(pk.numpy(), k_now.numpy(), average_method="arithmetic")
+                print(f"[Reuse Similarity] Step {ps}->{step}, Layer {layer_idx}, Head {h}: "
+                      f"Q={q_nmi:.4f}, K={k_nmi:.4f}, Avg={(q_nmi + k_nmi) / 2.0:.4f}")
+                out[h] = (ps, float(q_nmi), float(k_nmi))
+            hist.setdefault(key_, {})[step] = (q_now, k_now)
+        return out
 
     def _get_min_kc_ratio_for_heads_from_step(self, inference_step, num_heads):
         """Per-head ratios from the profile, clipped, or the scalar ratio (``:931-956``)."""

@@ -113,6 +113,98 @@ def test_reuse_schedule():
     assert p2.should_recluster()  # nothing cached yet -> forced
 
 
+def test_reuse_debug_trace(monkeypatch, capsys):
+    """SVG_REUSE_DEBUG prints the reference's [reuse] lines from kmeans_clustering's decision
+    (svoo/models/wan/attention.py:682-704); should_recluster() alone stays silent."""
+    p = _proc(start_reuse_step=2, reuse_interval=2)
+    p.current_inference_step = 3
+    monkeypatch.setenv("SVG_REUSE_DEBUG", "1")
+    assert p.should_recluster()
+    assert capsys.readouterr().out == ""
+    assert p.should_recluster(trace=True)  # offset 1: reuse, but nothing cached -> forced
+    assert capsys.readouterr().out.splitlines() == [
+        "[reuse] current_step=3, start_reuse_step=2, reuse_interval=2",
+        "[reuse] offset=1, should_recluster=False",
+        "[reuse] No cached clustering results, forcing recluster",
+    ]
+    p._cached_clustering_results = {"x": 1}
+    assert not p.should_recluster(trace=True)
+    assert capsys.readouterr().out.splitlines()[-1] == "[reuse] Reusing cached clustering results"
+    p.current_inference_step = 1  # before the reuse anchor: offset None, recluster
+    assert p.should_recluster(trace=True)
+    assert "[reuse] offset=None, should_recluster=True" in capsys.readouterr().out
+    monkeypatch.setenv("SVG_REUSE_DEBUG", "false")
+    p.should_recluster(trace=True)
+    assert capsys.readouterr().out == ""
+
+
+def test_reuse_similarity_report(monkeypatch, capsys):
+    """COMPUTE_REUSE_SIMILARITY: per (layer, head), the NMI of this clustering's labels against the previous
+    recorded step's (svoo/models/wan/attention.py:821-861), checked against a plug-in computation of NMI."""
+    r = np.random.default_rng(7)
+    n, heads = 500, 2
+    p = _proc()
+
+    def labels(seed):
+        g = np.random.default_rng(seed)
+        return {"qlabels": torch.from_numpy(g.integers(0, 8, (heads, n)).astype(np.int32)),
+                "klabels": torch.from_numpy(g.integers(0, 16, (heads, n)).astype(np.int32))}
+
+    def nmi(a, b):  # arithmetic-mean normalised mutual information from the contingency table
+        ua, ia = np.unique(a, return_inverse=True)
+        ub, ib = np.unique(b, return_inverse=True)
+        c = np.zeros((len(ua), len(ub)))
+        np.add.at(c, (ia, ib), 1.0)
+        pij = c / c.sum()
+        pi, pj = pij.sum(1), pij.sum(0)
+        nz = pij > 0
+        mi = (pij[nz] * np.log(pij[nz] / np.outer(pi, pj)[nz])).sum()
+        h = lambda q: -(q[q > 0] * np.log(q[q > 0])).sum()  # noqa: E731
+        return mi / ((h(pi) + h(pj)) / 2.0)
+
+    r1 = labels(1)
+    p.current_inference_step = 4
+    assert p.report_reuse_similarity(r1, 3, heads) == {}  # nothing earlier
+    r2 = labels(2)
+    # the second clustering keeps most labels of the first
+    keep = r.random((heads, n)) < 0.8
+    for k_ in ("qlabels", "klabels"):
+        r2[k_] = torch.where(torch.from_numpy(keep), r1[k_], r2[k_])
+    p.current_inference_step = 9
+    got = p.report_reuse_similarity(r2, 3, heads)
+    out = capsys.readouterr().out.splitlines()
+    assert len(out) == heads and out[0].startswith("[Reuse Similarity] Step 4->9, Layer 3, Head 0: Q=")
+    for h in range(heads):
+        ps, qn, kn = got[h]
+        assert ps == 4
+        assert qn == pytest.approx(nmi(r1["qlabels"][h].numpy(), r2["qlabels"][h].numpy()), rel=1e-9)
+        assert kn == pytest.approx(nmi(r1["klabels"][h].numpy(), r2["klabels"][h].numpy()), rel=1e-9)
+        assert 0.2 < qn < 1.0
+    # identical labels give 1
+    p.current_inference_step = 10
+    got = p.report_reuse_similarity(r2, 3, heads)
+    assert got[0][0] == 9 and got[0][1] == pytest.approx(1.0) and got[0][2] == pytest.approx(1.0)
+
+
+def test_save_qk_dump(monkeypatch, tmp_path):
+    """SAVE_QK writes {dir}/step{timestep}/layer{l}.pt with q, k, timestep, layer_idx from the scheduler
+    timestep SAVE_QK_START_STEP on (svoo/models/wan/attention.py:217-240)."""
+    from svoo_amd.processor import save_qk
+
+    q, k = torch.randn(1, 2, 6, 4), torch.randn(1, 2, 6, 4)
+    assert save_qk(q, k, torch.tensor([999.0]), 3) is None  # switched off
+    monkeypatch.setenv("SAVE_QK", "1")
+    assert save_qk(q, k, torch.tensor([999.0]), 3) is None  # no directory
+    monkeypatch.setenv("SAVE_QK_DIR", str(tmp_path))
+    monkeypatch.setenv("SAVE_QK_START_STEP", "500")
+    assert save_qk(q, k, torch.tensor([400.0]), 3) is None  # before the start step
+    assert save_qk(q, k, None, 3) is None  # dense (no timestep) calls are not captured
+    path = save_qk(q, k, torch.tensor([999.0, 999.0]), 3)
+    assert path == str(tmp_path / "step999.0" / "layer3.pt")
+    d = torch.load(path, weights_only=True)
+    assert torch.equal(d["q"], q) and torch.equal(d["k"], k) and d["timestep"] == 999.0 and d["layer_idx"] == 3
+
+
 def test_dynamic_ratio_from_profile():
     from svoo_amd.sparsity import SparsityLookup
 
