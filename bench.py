@@ -416,27 +416,52 @@ def kernel_table(step, cfg, h, nv, d, qcn, kcn, iters):
     out = {"per_kernel": dict(sorted(table.items(), key=lambda kv: -kv[1]["total_us"]))}
     bh = h
     stage = {}
-    for nm in ("cocluster_assign16_kernel", "cocluster_assign_kernel"):
-        ts = launches(nm)
-        if ts:
-            stage[nm] = {"key_side_avg_us": round(float(sum(ts[0::2]) / len(ts[0::2])), 2),
-                         "query_side_avg_us": round(float(sum(ts[1::2]) / max(1, len(ts[1::2]))), 2)}
-    a16 = launches("cocluster_assign16_kernel")
-    fb = launches("cocluster_assign_kernel")
-    if a16:
-        # launch order per call: key side, query side, per iteration; from the second iteration on the query
-        # side runs only on the tokens the pruning test left (cocluster_prune_kernel), so its HBM roofline is
-        # taken on the first iteration's full pass
-        key_us = (sum(a16[0::2]) + sum(fb[0::2])) / len(a16[0::2])
-        qry_full_us = a16[1] + (fb[1] if len(fb) > 1 else 0.0)
-        qry_later = [a + f for a, f in zip(a16[3::2], fb[3::2])]
+    # Passes of the co-clustering, in launch order: each starts with its prep kernel and alternates key side,
+    # query side.  A key-side pass from the second iteration on is the candidate pass (radius, lists, score
+    # kernels) when the library takes it, else the full pass; each ends with the hi/lo kernel on the tokens it
+    # left (cocluster_assign_kernel).
+    passes = []
+    for e in evs:
+        nm = short(e.name)
+        if nm.startswith("cocluster_prep"):
+            passes.append({"side": "key" if len(passes) % 2 == 0 else "query", "k": {}})
+        if passes and nm.startswith("cocluster_"):
+            passes[-1]["k"].setdefault(nm, []).append(e.time_range.elapsed_us())
+    tot = lambda pz, names: sum(sum(pz["k"].get(nm, [])) for nm in names)  # noqa: E731
+    key_passes = [pz for pz in passes if pz["side"] == "key"]
+    qry_passes = [pz for pz in passes if pz["side"] == "query"]
+    full_names = ("cocluster_assign16_kernel", "cocluster_assign_kernel")
+    cand_names = ("cocluster_nu_kernel", "cocluster_radius_kernel", "cocluster_lists_kernel",
+                  "cocluster_score_kernel", "cocluster_assign_kernel")
+    if key_passes and "cocluster_assign16_kernel" in key_passes[0]["k"]:
+        # the first key-side pass scores every cluster for every token: its MFMA roofline
+        key_us = tot(key_passes[0], full_names)
         key_flop = 2.0 * bh * nv * d * kcn
-        qry_bytes = bh * nv * (2 * d + 4)
         stage["assign_key_side"] = {"bound": "mfma", "achieved": round(key_flop / (key_us * 1e-6) / 1e12, 1),
                                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                     "frac": round(key_flop / (key_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                                    "avg_us_per_side": round(key_us, 2),
-                                    "note": "fp16 certified pass + hi/lo fallback; algorithmic FLOP of the reduced form"}
+                                    "full_pass_us": round(key_us, 2),
+                                    "fallback_us": round(tot(key_passes[0], ("cocluster_assign_kernel",)), 2),
+                                    "note": "first iteration: fp16 certified pass + hi/lo fallback; algorithmic "
+                                            "FLOP of the reduced form"}
+        cand = [pz for pz in key_passes[1:] if "cocluster_score_kernel" in pz["k"]]
+        full_later = [pz for pz in key_passes[1:] if "cocluster_assign16_kernel" in pz["k"]]
+        if cand:
+            avg = lambda names: round(sum(tot(pz, names) for pz in cand) / len(cand), 2)  # noqa: E731
+            stage["key_candidate_passes"] = {
+                "passes": len(cand), "avg_us": avg(cand_names),
+                "radius_us": avg(("cocluster_radius_kernel",)), "lists_us": avg(("cocluster_lists_kernel",)),
+                "score_us": avg(("cocluster_score_kernel",)), "fallback_us": avg(("cocluster_assign_kernel",)),
+                "note": "iterations 2+: triangle-inequality candidates in profile space, exact (same labels)"}
+        if full_later:
+            stage["key_full_passes_later_avg_us"] = round(
+                sum(tot(pz, full_names) for pz in full_later) / len(full_later), 2)
+    if qry_passes and "cocluster_assign16_kernel" in qry_passes[0]["k"]:
+        # the query side's later passes run only on the tokens the pruning test left, so its HBM roofline is
+        # taken on the first iteration's full pass
+        qry_full_us = tot(qry_passes[0], full_names)
+        qry_later = [tot(pz, full_names) for pz in qry_passes[1:]]
+        qry_bytes = bh * nv * (2 * d + 4)
         stage["assign_query_side"] = {"bound": "hbm", "achieved": round(qry_bytes / (qry_full_us * 1e-6) / 1e9, 1),
                                       "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                                       "frac": round(qry_bytes / (qry_full_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),

@@ -18,6 +18,11 @@
 // From the second iteration on the passes list the tokens whose label changed, and the centroid sums
 // are updated from that list alone (fp64; equal to a full recount while the sums are exact, see
 // centroid.hip), or recounted when many labels changed.
+// candidate pass (key side, second iteration on, at least 1000 key clusters): the triangle inequality in
+// profile space around each token's current label bounds which clusters can beat it; only those are scored
+// (radius, lists and score kernels below), the same labels as a full pass.
+#include <stdlib.h>
+
 #include "svoo_common.h"
 
 namespace svoo {
@@ -193,7 +198,10 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
                                                                   double* __restrict__ e_old,
                                                                   float* __restrict__ delta,
                                                                   uint32_t* __restrict__ delta_max,
-                                                                  int32_t* __restrict__ t_out, int have_old) {
+                                                                  int32_t* __restrict__ t_out, int have_old,
+                                                                  uint16_t* __restrict__ praw_out,
+                                                                  double* __restrict__ inv_out,
+                                                                  float* __restrict__ nrm_out) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int kpp = pm_kpp(kp), ps = kpp + 8;
   uint16_t* praw = (uint16_t*)smem;                             // [16][ps] bf16
@@ -239,9 +247,25 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
     }
 #pragma unroll
     for (int o = 8; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
-    if (sub == 0) inv[r] = 1.0 / sqrt(sq + 1e-8);
+    if (sub == 0) {
+      inv[r] = 1.0 / sqrt(sq + 1e-8);
+      // profile rows for the key side's candidate pass (kp <= 128): 1 / |praw| and |P|^2 = sq / (sq + 1e-8)
+      if (inv_out && r0 + r < jpad) {
+        inv_out[(size_t)bidx * jpad + r0 + r] = inv[r];
+        nrm_out[(size_t)bidx * jpad + r0 + r] = (float)(sq / (sq + 1e-8));
+      }
+    }
   }
   __syncthreads();
+  if (praw_out) {
+    // praw (exactly bf16) as [jpad][128] rows, zero past kp
+    for (int t = tid; t < kPmRows * 16; t += 256) {
+      const int r = t / 16, c = t % 16;
+      if (r0 + r < jpad)
+        *((u32x4_t*)(praw_out + ((size_t)bidx * jpad + r0 + r) * 128) + c) =
+            c * 8 < kpp ? *(const u32x4_t*)(praw + r * ps + c * 8) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
   if (profile) {
     const int nreal = max(0, min(kPmRows, j - r0));
     float* pb = profile + (size_t)bidx * j * kp;
@@ -901,6 +925,495 @@ __global__ void __launch_bounds__(256) cocluster_prune_kernel(const int32_t* __r
   }
 }
 
+// --------------------------------------------------------------------------------------- candidate pass
+// Exact pruning of a key-side pass by the triangle inequality in profile space.  The score of token x and
+// cluster j is x . E_j = P_j . y with y = C x (C the other side's centroids, kp <= 128 of them) and P_j the
+// profile rows, unit vectors up to |P_j|^2 = n_j = sq / (sq + 1e-8).  With u = y / |y|, d_a = |u - P_a| for
+// the token's current label a (its anchor) and D_aj = |P_a - P_j|:
+//   D_aj >= 2 d_a + m   implies   u . P_a - u . P_j >= (m^2 - nu) / 2,   nu >= max_j n_j - n_a,
+// so such a cluster scores at least |y| (m^2 - nu) / 2 below the anchor.  m is chosen per token so that this
+// exceeds twice |x| eps_E, the difference between the exact score and the one the prep's E defines (fp32
+// sums in its phase 3, eps_E <= 2^-16 ||C||_F): those clusters are then strictly below the anchor in the
+// scores that define the label.  Three kernels per pass:
+//   radius: per token T = 2 d_a + m from |y| (y on the MFMA) and the anchor's score, as rigorous upper
+//           bounds; the cluster's radius is the maximum over its tokens;
+//   lists:  per cluster a, the clusters with D_aj below its radius (D from the exactly-bf16 raw profiles on
+//           the MFMA, lowered by 2^-14 against the fp32 sums), at most kCandList of them;
+//   score:  per 64 label-sorted tokens (one wave, few anchors), the union of their anchors' lists scored on
+//           the hi + lo MFMA (within e = 2^-15 |x| Emax of x . E); the best is certified when it beats the
+//           second by more than 2 e: it is then the exact argmax of x . E, the label every other pass of this
+//           file gives such a token.  The others (near ties, long lists, a zero y) go to the head's fallback
+//           list for the hi + lo kernel.
+constexpr int kCandList = 32;   // list entries per cluster
+constexpr int kCandUnion = 128; // clusters a wave scores (4 tiles of 32)
+constexpr int kCandMaxJ = 4096; // clusters per side (the library's limit)
+
+// Upper bound on the radius T = 2 d_a + m of one token (both lanes of the token call it with the same
+// arguments); -1 when the token cannot be bounded (no anchor, y too small, a non-finite value).
+__device__ __forceinline__ float cand_radius(float s_a, float yn, float xnu, float cfro, float emax, float n_a,
+                                             float nu) {
+  const float etok = 0x1p-15f * xnu * emax;  // |s~_a - x . E_a|
+  const float epsx = 0x1p-16f * cfro * xnu;   // |x| eps_E, and |y~ - y| without the norm's rounding
+  const float epsy = epsx + 0x1p-17f * yn;
+  const float yl = yn - epsy, yu = yn + epsy;
+  const float slo = s_a - etok - epsx;  // lower bound on P_a . y
+  float ratio = slo >= 0.0f ? slo / yu : slo / yl;
+  ratio -= 0x1p-20f * fabsf(ratio) + 0x1p-40f;
+  const float d2 = (1.0f + n_a - 2.0f * ratio) * (1.0f + 0x1p-20f) + 0x1p-40f;
+  const float dup = sqrtf(fmaxf(d2, 0.0f)) * (1.0f + 0x1p-20f);
+  const float m = sqrtf((4.0f * epsx / yl + nu) * (1.0f + 0x1p-20f) + 0x1p-40f) * (1.0f + 0x1p-20f);
+  const float t = 2.0f * dup + m;
+  return (yl > 0.0f && t < INFINITY) ? t : -1.0f;  // -1 also for NaN
+}
+
+// bf16 pairs: a.x b.x + a.y b.y + c on v_dot2_f32_bf16 (exact products, fp32 sums)
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Token operands of TB 32-token blocks (lane l and l + 32 hold the halves of token l of a block), |x|^2.
+template <int TB>
+__device__ __forceinline__ void cand_tokens(const uint16_t* xb, const int32_t* tok, int h, u32x4_t (*xop)[8],
+                                            float* xn2) {
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    const u32x4_t* src = (const u32x4_t*)(xb + (size_t)tok[cb] * 128);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) xop[cb][ks] = src[ks * 2 + h];
+  }
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    float q2 = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q2 = dot2_bf16(xop[cb][ks][e], xop[cb][ks][e], q2);
+    xn2[cb] = q2 + __shfl_xor(q2, 32);
+  }
+}
+
+// Upper bound on E's row norms: |2^t E_j| <= |E16_j| + |2^t E_j - E16_j|.
+__device__ __forceinline__ float cand_emax(const uint32_t* norm_max, const uint32_t* err_max, const int32_t* t_head,
+                                           int bidx) {
+  return __builtin_amdgcn_ldexpf(__uint_as_float(norm_max[bidx]) + __uint_as_float(err_max[bidx]), -t_head[bidx]) *
+         (1.0f + 0x1p-20f);
+}
+
+// Value of token slot `lane` of a wave (lanes 0-31: block 0, lanes 32-63: block 1 when TB == 2); the two
+// lanes of a token hold the same value.
+template <int TB, typename T>
+__device__ __forceinline__ T cand_slot(const T* v, int h, int l32) {
+  if constexpr (TB == 1) {
+    return v[0];
+  } else {
+    const T v1 = __shfl(v[1], l32);
+    return h == 0 ? v[0] : v1;
+  }
+}
+
+constexpr int kCandTB = 1;                  // token blocks of 32 per wave
+constexpr int kCandWaveTok = 32 * kCandTB;  // label-sorted positions per wave
+constexpr int kCandBlockTok = 4 * kCandWaveTok;
+
+// radius: one wave per kCandWaveTok consecutive positions of the head's label-sorted order.  Writes, per
+// position, the token's anchor and radius (or -1) and the cluster maxima to trad (float bits, zero on entry),
+// one atomic per distinct anchor of a wave.  C is staged in LDS once per block (16-byte chunk c of row r at
+// chunk swz(r, c)).
+__global__ void __launch_bounds__(256) cocluster_radius_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ cother, const uint16_t* __restrict__ e_hi,
+    const uint16_t* __restrict__ e_lo, const float* __restrict__ nrm, const uint32_t* __restrict__ nu_bits,
+    const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max, const int32_t* __restrict__ t_head,
+    const int32_t* __restrict__ sorted_idx, const int32_t* __restrict__ labels, int n, int j, int jpad, int ko,
+    float* __restrict__ pos_t, int32_t* __restrict__ pos_anc, uint32_t* __restrict__ trad) {
+  constexpr int TB = kCandTB;
+  __shared__ __attribute__((aligned(16))) uint16_t s_c[128 * 128];
+  __shared__ float s_cf[4];
+  const int bidx = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, h = lane / 32,
+            l32 = lane % 32;
+  const int p0 = blockIdx.x * kCandBlockTok + wave * kCandWaveTok;
+  const uint16_t* cb_base = cother + (size_t)bidx * ko * 128;
+  int tok[TB], anc[TB];
+  bool inpos[TB], vt[TB];
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    inpos[cb] = p0 + cb * 32 + l32 < n;
+    tok[cb] = sorted_idx[(size_t)bidx * n + min(p0 + cb * 32 + l32, n - 1)];
+  }
+  {
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + 256 * i, r = c / 16, ch = c % 16;
+      const u32x4_t w = r < ko ? ((const u32x4_t*)cb_base)[c] : u32x4_t{0u, 0u, 0u, 0u};
+      *(u32x4_t*)(s_c + r * 128 + swz(r, ch) * 8) = w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sq = dot2_bf16(w[e], w[e], sq);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+    if (lane == 0) s_cf[wave] = sq;
+  }
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    anc[cb] = labels[(size_t)bidx * n + tok[cb]];
+    vt[cb] = inpos[cb] && anc[cb] >= 0 && anc[cb] < j;
+    if (!vt[cb]) anc[cb] = 0;
+  }
+  u32x4_t xop[TB][8];
+  float xn2[TB];
+  cand_tokens<TB>(x + (size_t)bidx * n * 128, tok, h, xop, xn2);
+  __syncthreads();
+  if (p0 >= n) return;
+  const float cfro = sqrtf((s_cf[0] + s_cf[1] + s_cf[2] + s_cf[3]) * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
+  // anchor scores on v_dot2_f32_bf16: the lane's 64 components of x against E_hi + E_lo of the anchor
+  float sa[TB];
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    const u32x4_t* hr = (const u32x4_t*)(e_hi + ((size_t)bidx * jpad + anc[cb]) * 128);
+    const u32x4_t* lr = (const u32x4_t*)(e_lo + ((size_t)bidx * jpad + anc[cb]) * 128);
+    float acc = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const u32x4_t wh = hr[ks * 2 + h], wl = lr[ks * 2 + h];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = dot2_bf16(xop[cb][ks][e], wl[e], dot2_bf16(xop[cb][ks][e], wh[e], acc));
+    }
+    sa[cb] = acc + __shfl_xor(acc, 32);
+  }
+  // |y|^2 on the MFMA (C rows past ko are zero)
+  float ysq[TB];
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) ysq[cb] = 0.0f;
+  for (int ct = 0; ct * 32 < ko; ++ct) {
+    const int crow = ct * 32 + l32;
+    u32x4_t ca[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) ca[ks] = *(const u32x4_t*)(s_c + crow * 128 + swz(crow, ks * 2 + h) * 8);
+#pragma unroll
+    for (int cb = 0; cb < TB; ++cb) {
+      f32x16_t acc = {};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) acc = mfma32x32x16(as_bf16x8(ca[ks]), as_bf16x8(xop[cb][ks]), acc);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ysq[cb] = fmaf(acc[r], acc[r], ysq[cb]);
+    }
+  }
+  const float emax = cand_emax(norm_max, err_max, t_head, bidx);
+  const float nu = __uint_as_float(nu_bits[bidx]);
+  float tr[TB];
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    const float yn = sqrtf(ysq[cb] + __shfl_xor(ysq[cb], 32));
+    const float xnu = sqrtf(xn2[cb] * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
+    tr[cb] = vt[cb] ? cand_radius(sa[cb], yn, xnu, cfro, emax, nrm[(size_t)bidx * jpad + anc[cb]], nu) : -1.0f;
+    if (inpos[cb] && h == 0) {
+      const size_t o = (size_t)bidx * n + p0 + cb * 32 + l32;
+      pos_t[o] = tr[cb];
+      pos_anc[o] = vt[cb] ? anc[cb] : -1;
+    }
+  }
+  // cluster maxima: one atomic per distinct anchor of the wave
+  const int myanc = cand_slot<TB>(anc, h, l32);
+  const float myt0 = cand_slot<TB>(tr, h, l32);
+  const float myt = (TB == 1 && h == 1) ? -1.0f : myt0;
+  uint64_t todo = __ballot(myt > 0.0f);
+  while (todo) {
+    const int first = __builtin_ctzll(todo);
+    const int a = __shfl(myanc, first);
+    const uint64_t same = __ballot(myt > 0.0f && myanc == a);
+    float mx = (same >> lane) & 1 ? myt : 0.0f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == first) atomicMax(trad + (size_t)bidx * jpad + a, __float_as_uint(mx));
+    todo &= ~same;
+  }
+}
+
+// lists: one block per 32-row strip of a head; each wave keeps the strip's raw-profile operand and takes every
+// 4th 32-column tile: D_aj^2 >= n_a + n_j - 2 inv_a inv_j (praw_a . praw_j) - 2^-14, and cluster j joins a's
+// list when that is below a's squared radius.  A list that would be longer than kCandList keeps its count.
+__global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __restrict__ praw,
+                                                              const double* __restrict__ inv,
+                                                              const float* __restrict__ nrm,
+                                                              const uint32_t* __restrict__ trad, int j, int jpad,
+                                                              int16_t* __restrict__ lists,
+                                                              int32_t* __restrict__ list_n) {
+  __shared__ int cnt[32];
+  __shared__ int16_t lst[32][kCandList];
+  const int bidx = blockIdx.y, ta = blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave,
+            h = lane / 32, l32 = lane % 32;
+  const int nt = jpad / 32;
+  if (tid < 32) cnt[tid] = 0;
+  const uint16_t* pb = praw + (size_t)bidx * jpad * 128;
+  const double* ib = inv + (size_t)bidx * jpad;
+  const float* nb = nrm + (size_t)bidx * jpad;
+  u32x4_t aop[8];
+  const u32x4_t* arow = (const u32x4_t*)(pb + (size_t)(ta * 32 + l32) * 128);
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) aop[ks] = arow[ks * 2 + h];
+  double ia[16];
+  float na[16], th[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int a = ta * 32 + (r / 4) * 8 + h * 4 + r % 4;
+    ia[r] = ib[a];
+    na[r] = nb[a];
+    const float t = __uint_as_float(trad[(size_t)bidx * jpad + a]);
+    th[r] = a < j ? t * t : 0.0f;
+  }
+  __syncthreads();
+  for (int tj = wave; tj < nt; tj += 4) {
+    const u32x4_t* brow = (const u32x4_t*)(pb + (size_t)(tj * 32 + l32) * 128);
+    u32x4_t bop[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) bop[ks] = brow[ks * 2 + h];
+    f32x16_t acc = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) acc = mfma32x32x16(as_bf16x8(aop[ks]), as_bf16x8(bop[ks]), acc);
+    const int jj = tj * 32 + l32;
+    const double ij = ib[jj], nj = (double)nb[jj];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float d2 = (float)((double)na[r] + nj - 2.0 * ((double)acc[r] * ia[r] * ij) - 0x1p-14);
+      if (jj < j && d2 < th[r]) {
+        const int al = (r / 4) * 8 + h * 4 + r % 4;
+        const int slot = atomicAdd(&cnt[al], 1);
+        if (slot < kCandList) lst[al][slot] = (int16_t)jj;
+      }
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < 32 * kCandList; t += 256) {
+    const int al = t / kCandList, e = t % kCandList;
+    const int a = ta * 32 + al;
+    lists[((size_t)bidx * jpad + a) * kCandList + e] = e < cnt[al] ? lst[al][e] : (int16_t)-1;
+  }
+  if (tid < 32) list_n[(size_t)bidx * jpad + ta * 32 + tid] = cnt[tid];
+}
+
+// nu of each head: twice the largest |1 - n_a| over its real rows (nu_bits zero on entry).
+__global__ void __launch_bounds__(256) cocluster_nu_kernel(const float* __restrict__ nrm, int j, int jpad,
+                                                           uint32_t* __restrict__ nu_bits) {
+  const int bidx = blockIdx.y;
+  float dv = 0.0f;
+  for (int a = threadIdx.x; a < j; a += 256) dv = fmaxf(dv, fabsf(1.0f - nrm[(size_t)bidx * jpad + a]));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) dv = fmaxf(dv, __shfl_xor(dv, o));
+  if (threadIdx.x % kWave == 0) atomicMax(nu_bits + bidx, __float_as_uint(2.0f * dv * (1.0f + 0x1p-20f) + 0x1p-40f));
+}
+
+// score: one wave per kCandWaveTok consecutive label-sorted positions, as in the radius kernel, whose
+// per-position anchors and radii it reads.  The wave's distinct anchors (usually one or two) bring their lists;
+// the union (a bitmap in the wave's LDS, then compacted in cluster order) is scored on the hi + lo MFMA 32
+// clusters at a time.  One reservation per block and list.
+__global__ void __launch_bounds__(256) cocluster_score_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi, const uint16_t* __restrict__ e_lo,
+    const int16_t* __restrict__ lists, const int32_t* __restrict__ list_n, const float* __restrict__ pos_t,
+    const int32_t* __restrict__ pos_anc, const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max,
+    const int32_t* __restrict__ t_head, const int32_t* __restrict__ sorted_idx, int32_t* __restrict__ labels, int n,
+    int j, int jpad, int2* __restrict__ changes, int32_t* __restrict__ nchanges, int32_t* __restrict__ fb_list,
+    int32_t* __restrict__ fb_count) {
+  constexpr int TB = kCandTB;
+  __shared__ uint32_t s_bm[4][kCandMaxJ / 32];
+  __shared__ int16_t s_u[4][kCandUnion];
+  __shared__ int s_cnt[2][4], s_base[2];
+  const int bidx = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, h = lane / 32,
+            l32 = lane % 32;
+  const int p0 = blockIdx.x * kCandBlockTok + wave * kCandWaveTok;
+  const bool wv = p0 < n;  // the wave has positions (the block's reservations below need every wave)
+  uint32_t* bm = s_bm[wave];
+  int16_t* ul = s_u[wave];
+  const int nw = (j + 31) / 32;  // bitmap words in use
+  for (int w = lane; w < nw; w += kWave) bm[w] = 0u;
+  int tok[TB], anc[TB];
+  bool inpos[TB], vt[TB];
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    const int pos = p0 + cb * 32 + l32;
+    inpos[cb] = pos < n;
+    const size_t o = (size_t)bidx * n + min(pos, n - 1);
+    tok[cb] = sorted_idx[o];
+    anc[cb] = pos_anc[o];
+    vt[cb] = inpos[cb] && anc[cb] >= 0 && pos_t[o] > 0.0f;
+    if (!vt[cb]) anc[cb] = 0;
+  }
+  // distinct anchors: lane k < nd holds the k-th
+  const int myanc = cand_slot<TB>(anc, h, l32);
+  const bool myv0 = cand_slot<TB>(vt, h, l32);
+  const bool myv = myv0 && !(TB == 1 && h == 1);
+  uint64_t todo = __ballot(myv);
+  int da = -1, nd = 0;
+  while (todo) {
+    const int first = __builtin_ctzll(todo);
+    const int a = __shfl(myanc, first);
+    if (lane == nd) da = a;
+    ++nd;
+    todo &= ~__ballot(myv && myanc == a);
+  }
+  int ln = 0;
+  int16_t ent[kCandList];
+  if (da >= 0) {
+    ln = list_n[(size_t)bidx * jpad + da];
+    const int16_t* lp = lists + ((size_t)bidx * jpad + da) * kCandList;
+#pragma unroll
+    for (int e = 0; e < kCandList; e += 8) *(u32x4_t*)&ent[e] = *(const u32x4_t*)&lp[e];
+  }
+  u32x4_t xop[TB][8];
+  float xn2[TB];
+  if (wv) cand_tokens<TB>(x + (size_t)bidx * n * 128, tok, h, xop, xn2);
+  // the anchors' lists into the bitmap (a list longer than kCandList leaves its tokens to the fallback)
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the bitmap is clear
+  if (da >= 0 && ln <= kCandList) {
+#pragma unroll
+    for (int e = 0; e < kCandList; ++e)
+      if (e < ln) atomicOr(&bm[ent[e] >> 5], 1u << (ent[e] & 31));
+  }
+  // per token: its anchor's list fitted
+  bool lok[TB];
+  {
+    const uint64_t longm = __ballot(da >= 0 && ln > kCandList);
+#pragma unroll
+    for (int cb = 0; cb < TB; ++cb) {
+      bool bad = false;
+      uint64_t m = longm;
+      while (m) {
+        const int dk = __shfl(da, __builtin_ctzll(m));  // every lane takes part in the exchange
+        bad = bad || anc[cb] == dk;
+        m &= m - 1;
+      }
+      lok[cb] = !bad;
+    }
+  }
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the bitmap is complete
+  // compact the union in cluster order
+  int nu = 0;
+  {
+    const uint32_t w0 = 2 * lane < nw ? bm[2 * lane] : 0u, w1 = 2 * lane + 1 < nw ? bm[2 * lane + 1] : 0u;
+    const int c = __popc(w0) + __popc(w1);
+    int inc = c;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int u = __shfl_up(inc, o);
+      if (lane >= o) inc += u;
+    }
+    nu = __shfl(inc, kWave - 1);
+    int idx = inc - c;
+    for (uint32_t w = w0, base = 64 * lane; w; w &= w - 1) {
+      if (idx < kCandUnion) ul[idx] = (int16_t)(base + __builtin_ctz(w));
+      ++idx;
+    }
+    for (uint32_t w = w1, base = 64 * lane + 32; w; w &= w - 1) {
+      if (idx < kCandUnion) ul[idx] = (int16_t)(base + __builtin_ctz(w));
+      ++idx;
+    }
+  }
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const bool uover = nu > kCandUnion;
+  float b1[TB], b2[TB];
+  int c1[TB];
+  bool fin[TB];
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    b1[cb] = -INFINITY;
+    b2[cb] = -INFINITY;
+    c1[cb] = -1;
+    fin[cb] = true;
+  }
+  if (wv && !uover) {
+    const uint16_t* eh = e_hi + (size_t)bidx * jpad * 128;
+    const uint16_t* el = e_lo + (size_t)bidx * jpad * 128;
+    for (int ut = 0; ut * 32 < nu; ++ut) {
+      const int ui = ut * 32 + l32;
+      const int crow = ul[ui < nu ? ui : 0];
+      const u32x4_t* hrow = (const u32x4_t*)(eh + (size_t)crow * 128) + h;
+      const u32x4_t* lrow = (const u32x4_t*)(el + (size_t)crow * 128) + h;
+      u32x4_t ph[8], pl[8];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        ph[ks] = hrow[ks * 2];
+        pl[ks] = lrow[ks * 2];
+      }
+#pragma unroll
+      for (int cb = 0; cb < TB; ++cb) {
+        f32x16_t acc = {};
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          acc = mfma32x32x16(as_bf16x8(ph[ks]), as_bf16x8(xop[cb][ks]), acc);
+          acc = mfma32x32x16(as_bf16x8(pl[ks]), as_bf16x8(xop[cb][ks]), acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = ut * 32 + (r / 4) * 8 + h * 4 + r % 4;
+          const float sv = acc[r];
+          if (row < nu) {
+            fin[cb] = fin[cb] && (sv > -INFINITY && sv < INFINITY);
+            if (sv > b1[cb]) {
+              b2[cb] = b1[cb];
+              b1[cb] = sv;
+              c1[cb] = ul[row];
+            } else if (sv > b2[cb]) {
+              b2[cb] = sv;
+            }
+          }
+        }
+      }
+    }
+  }
+  const float emax = cand_emax(norm_max, err_max, t_head, bidx);
+  int lab[TB];
+  bool cert[TB];
+  uint64_t fbm[TB], chm[TB];
+  int nfb = 0, nch = 0;
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    const float o1 = __shfl_xor(b1[cb], 32), o2 = __shfl_xor(b2[cb], 32);
+    const int oc = __shfl_xor(c1[cb], 32);
+    const bool ofin = __shfl_xor((int)fin[cb], 32) != 0;
+    const float best = fmaxf(b1[cb], o1);
+    const float second = fmaxf(fminf(b1[cb], o1), fmaxf(b2[cb], o2));
+    lab[cb] = b1[cb] > o1 ? c1[cb] : oc;
+    const float xnu = wv ? sqrtf(xn2[cb] * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f) : 0.0f;
+    const float etok = 0x1p-15f * xnu * emax;
+    // b1 == o1 is a tie of two clusters (second == best): not certified
+    cert[cb] = vt[cb] && lok[cb] && !uover && fin[cb] && ofin && (best - second) > 2.0f * etok && lab[cb] >= 0;
+    const bool mine = inpos[cb] && h == 0;
+    fbm[cb] = __ballot(mine && !cert[cb]);
+    chm[cb] = __ballot(mine && cert[cb] && lab[cb] != anc[cb]);
+    nfb += (int)__popcll(fbm[cb]);
+    nch += (int)__popcll(chm[cb]);
+  }
+  if (lane == 0) {
+    s_cnt[0][wave] = nfb;
+    s_cnt[1][wave] = nch;
+  }
+  __syncthreads();
+  if (lane == 0 && wave < 2) {
+    const int tot = s_cnt[wave][0] + s_cnt[wave][1] + s_cnt[wave][2] + s_cnt[wave][3];
+    int base = 0;
+    if (tot > 0 && wave == 0) base = atomicAdd(fb_count + (size_t)bidx * kCounterStride, tot);
+    if (tot > 0 && wave == 1) base = atomicAdd(nchanges, tot);
+    s_base[wave] = base;
+  }
+  __syncthreads();
+  int fbase = s_base[0], cbase = s_base[1];
+  for (int w = 0; w < wave; ++w) {
+    fbase += s_cnt[0][w];
+    cbase += s_cnt[1][w];
+  }
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) {
+    const bool mine = inpos[cb] && h == 0;
+    if (mine && !cert[cb]) fb_list[(size_t)bidx * n + fbase + mask_rank(fbm[cb])] = tok[cb];
+    if (mine && cert[cb]) {
+      if (lab[cb] != anc[cb])
+        changes[cbase + mask_rank(chm[cb])] = make_int2(bidx * n + tok[cb], (anc[cb] << 16) | lab[cb]);
+      labels[(size_t)bidx * n + tok[cb]] = lab[cb];
+    }
+    fbase += (int)__popcll(fbm[cb]);
+    cbase += (int)__popcll(chm[cb]);
+  }
+}
+
 }  // namespace svoo
 
 using namespace svoo;
@@ -937,11 +1450,12 @@ static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uin
                        int j, int kp, int jpad, hipStream_t stream, uint16_t* e16 = nullptr,
                        uint32_t* err_max = nullptr, uint32_t* norm_max = nullptr, double* e_old = nullptr,
                        float* delta = nullptr, uint32_t* delta_max = nullptr, int32_t* t_out = nullptr,
-                       int have_old = 0) {
+                       int have_old = 0, uint16_t* praw_out = nullptr, double* inv_out = nullptr,
+                       float* nrm_out = nullptr) {
   if (kp <= kPmMaxKp) {
     hipLaunchKernelGGL(cocluster_prep_mfma_kernel, dim3(jpad / kPmRows, bh), dim3(256), pm_smem(kp), stream, a, b,
                        e_hi, e_lo, profile, j, kp, jpad, e16, err_max, norm_max, e_old, delta, delta_max, t_out,
-                       have_old);
+                       have_old, praw_out, inv_out, nrm_out);
     return check_launch("svoo_cocluster_prep");
   }
   // Wide profiles: the vector kernel.  Few rows -> 2 rows per block for more blocks; many -> 8.
@@ -992,6 +1506,21 @@ static const int kMaxClusters = 4096;
 // (1000 clusters, whose top-two gaps are small against the centroid moves).
 static const bool kPruneQueries = true;
 static const bool kPruneKeys = false;
+// The key side's candidate pass (radius, lists and score kernels) replaces the full pass from the second
+// iteration on when the query centroids fit one 128-row operand and there are at least kCandMinKc key clusters.
+// Its cost hardly depends on the cluster count while the full pass's grows with it; measured at the Wan shapes
+// (same labels either way): 500 key clusters, 1.29 ms full against 1.44 ms with it per 5-iteration clustering;
+// 1000 key clusters, 6.47 against 6.29 ms.  SVOO_KEY_CANDIDATES=0 / 1 in the environment switches it off / on
+// whatever the shape (comparisons and tests).
+static const int kCandMaxKp = 128;
+static const int kCandMinKc = 1000;
+static bool key_candidates_enabled(int qc, int kc) {
+  if (qc > kCandMaxKp) return false;
+  const char* v = getenv("SVOO_KEY_CANDIDATES");
+  if (v && v[0] == '0' && v[1] == 0) return false;
+  if (v && v[0] == '1' && v[1] == 0) return true;
+  return kc >= kCandMinKc;
+}
 
 extern "C" int svoo_cocluster_prep(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uint16_t* e_lo,
                                    float* profile, int bh, int j, int kp, int d, int jpad, void* stream) {
@@ -1031,9 +1560,16 @@ extern "C" int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, co
 //   delta_k/q    [bh][jpad_k/q] fp32         (per-row change of E since that pass)
 //   bnd_k/q      [3][bh][n] fp32             (per-token pruning bounds of each side)
 //   plist        [bh][n] int32               (tokens the pruning test left to the assignment pass)
+// and for the key side's candidate pass (qc <= 128 only; bnd_k's first two planes hold the radius and the
+// anchor of each label-sorted position):
+//   praw_k       [bh][jpad_k][128] bf16      (raw key-centroid profiles)
+//   inv_k        [bh][jpad_k] fp64, nrm_k [bh][jpad_k] fp32   (1 / |praw|, |P|^2)
+//   trad_k       [bh][jpad_k] fp32 bits      (cluster radii)
+//   lists_k      [bh][jpad_k][kCandList] int16, list_n_k [bh][jpad_k] int32   (candidate lists)
 struct CoClusterWs {
   size_t e_off, counts_off, sums_off, slab_off, sums_q_off, changes_off, nchanges_off, e16_off, fb_off, stats_off,
-      eold_k_off, eold_q_off, delta_k_off, delta_q_off, bnd_k_off, bnd_q_off, plist_off, total;
+      eold_k_off, eold_q_off, delta_k_off, delta_q_off, bnd_k_off, bnd_q_off, plist_off, praw_off, inv_off, nrm_off,
+      trad_off, lists_off, listn_off, total;
 };
 
 static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
@@ -1054,14 +1590,21 @@ static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
   w.fb_off = w.e16_off + e_bytes;
   w.stats_off = w.fb_off + al((size_t)bh * n * sizeof(int32_t));
   const int jk = pad_to(kc, kAssignChunk), jq = pad_to(qc, kAssignChunk);
-  w.eold_k_off = w.stats_off + al((size_t)(2 * kCounterStride + 4) * bh * sizeof(uint32_t));
+  w.eold_k_off = w.stats_off + al((size_t)(2 * kCounterStride + 5) * bh * sizeof(uint32_t));
   w.eold_q_off = w.eold_k_off + al((size_t)bh * jk * 128 * sizeof(double));
   w.delta_k_off = w.eold_q_off + al((size_t)bh * jq * 128 * sizeof(double));
   w.delta_q_off = w.delta_k_off + al((size_t)bh * jk * sizeof(float));
   w.bnd_k_off = w.delta_q_off + al((size_t)bh * jq * sizeof(float));
   w.bnd_q_off = w.bnd_k_off + al((size_t)3 * bh * n * sizeof(float));
   w.plist_off = w.bnd_q_off + al((size_t)3 * bh * n * sizeof(float));
-  w.total = w.plist_off + al((size_t)bh * n * sizeof(int32_t));
+  w.praw_off = w.plist_off + al((size_t)bh * n * sizeof(int32_t));
+  const bool cand = qc <= kCandMaxKp;
+  w.inv_off = w.praw_off + (cand ? al((size_t)bh * jk * 128 * sizeof(uint16_t)) : 0);
+  w.nrm_off = w.inv_off + (cand ? al((size_t)bh * jk * sizeof(double)) : 0);
+  w.trad_off = w.nrm_off + (cand ? al((size_t)bh * jk * sizeof(float)) : 0);
+  w.lists_off = w.trad_off + (cand ? al((size_t)bh * jk * sizeof(uint32_t)) : 0);
+  w.listn_off = w.lists_off + (cand ? al((size_t)bh * jk * kCandList * sizeof(int16_t)) : 0);
+  w.total = w.listn_off + (cand ? al((size_t)bh * jk * sizeof(int32_t)) : 0);
   return w;
 }
 
@@ -1110,7 +1653,8 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   uint32_t* norm_max = err_max + bh;
   uint32_t* delta_max = norm_max + bh;
   int32_t* t_head = (int32_t*)(delta_max + bh);
-  const size_t stats_words = (size_t)(2 * kCounterStride + 4) * bh;
+  uint32_t* nu_bits = (uint32_t*)(t_head + bh);
+  const size_t stats_words = (size_t)(2 * kCounterStride + 5) * bh;
   double* eold_k = (double*)(base + lay.eold_k_off);
   double* eold_q = (double*)(base + lay.eold_q_off);
   float* delta_k = (float*)(base + lay.delta_k_off);
@@ -1118,6 +1662,13 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   float* bnd_k = (float*)(base + lay.bnd_k_off);
   float* bnd_q = (float*)(base + lay.bnd_q_off);
   int32_t* plist = (int32_t*)(base + lay.plist_off);
+  uint16_t* praw_k = (uint16_t*)(base + lay.praw_off);
+  double* inv_k = (double*)(base + lay.inv_off);
+  float* nrm_k = (float*)(base + lay.nrm_off);
+  uint32_t* trad_k = (uint32_t*)(base + lay.trad_off);
+  int16_t* lists_k = (int16_t*)(base + lay.lists_off);
+  int32_t* listn_k = (int32_t*)(base + lay.listn_off);
+  const bool key_cand = key_candidates_enabled(qc, kc);
   // changed tokens above which an iteration recounts every cluster instead of moving the changed ones
   const int limit = (int)((long long)bh * n / 32);
   const int jpad_k = pad_to(kc, kAssignChunk), jpad_q = pad_to(qc, kAssignChunk);
@@ -1132,19 +1683,39 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   // label provably cannot change are skipped (cocluster_prune_kernel) and the pass runs on the rest.
   auto side = [&](const uint16_t* x, uint16_t* cent, const uint16_t* other, int32_t* labels, int32_t* sizes,
                   int32_t* sorted_idx, int32_t* offsets, double* sums, int kx, int ko, int jpad, int32_t* cnt,
-                  bool first, bool prune, double* eold, float* delta, float* bnd) -> int {
+                  bool first, bool prune, double* eold, float* delta, float* bnd, bool cand) -> int {
     int r;
     // The certified fp16 pass needs the fp16 copy of E, which the fp64-MFMA prep writes (profile widths up
     // to kPmMaxKp); wider profiles run the hi + lo kernel on every token.
     const bool fp16 = ko <= kPmMaxKp;
     const bool pr = fp16 && prune;
+    // candidate pass: from the second iteration on, over the label order of the last sort
+    const bool cp = cand && fp16 && ko <= kCandMaxKp && !first;
     if (fp16 && (r = svoo_zero_i32((int32_t*)stats, (long long)stats_words, s))) return r;
     if ((r = prep_launch(cent, other, e_hi, e_lo, nullptr, bh, kx, ko, jpad, s, fp16 ? e16 : nullptr, err_max,
-                         norm_max, pr ? eold : nullptr, delta, delta_max, t_head, first ? 0 : 1)))
+                         norm_max, pr ? eold : nullptr, delta, delta_max, t_head, first ? 0 : 1,
+                         cp ? praw_k : nullptr, cp ? inv_k : nullptr, cp ? nrm_k : nullptr)))
       return r;
     int2* chg = first ? nullptr : changes;
     int32_t* nc = first ? nullptr : cnt;
-    if (pr && !first) {
+    if (cp) {
+      const dim3 tgrid((n + kCandBlockTok - 1) / kCandBlockTok, bh);
+      float* pos_t = bnd;                              // plane 0
+      int32_t* pos_anc = (int32_t*)(bnd + (size_t)bh * n);  // plane 1
+      hipLaunchKernelGGL(cocluster_nu_kernel, dim3(1, bh), dim3(256), 0, s, nrm_k, kx, jpad, nu_bits);
+      if ((r = check_launch("svoo_co_cluster (nu)"))) return r;
+      if ((r = svoo_zero_i32((int32_t*)trad_k, (long long)bh * jpad, s))) return r;
+      hipLaunchKernelGGL(cocluster_radius_kernel, tgrid, dim3(256), 0, s, x, other, e_hi, e_lo, nrm_k, nu_bits, err_max,
+                         norm_max, t_head, sorted_idx, labels, n, kx, jpad, ko, pos_t, pos_anc, trad_k);
+      if ((r = check_launch("svoo_co_cluster (radius)"))) return r;
+      hipLaunchKernelGGL(cocluster_lists_kernel, dim3(jpad / 32, bh), dim3(256), 0, s, praw_k, inv_k, nrm_k, trad_k, kx,
+                         jpad, lists_k, listn_k);
+      if ((r = check_launch("svoo_co_cluster (lists)"))) return r;
+      hipLaunchKernelGGL(cocluster_score_kernel, tgrid, dim3(256), 0, s, x, e_hi, e_lo, lists_k, listn_k, pos_t, pos_anc,
+                         err_max, norm_max, t_head, sorted_idx, labels, n, kx, jpad, changes, cnt, fb_list, fb_count);
+      if ((r = check_launch("svoo_co_cluster (candidates)"))) return r;
+      r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s, changes, cnt, fb_list, fb_count);
+    } else if (pr && !first) {
       hipLaunchKernelGGL(cocluster_prune_kernel, dim3((n + 256 * kPruneSub - 1) / (256 * kPruneSub), bh), dim3(256),
                          0, s, labels, bnd, delta, delta_max, n, jpad, plist, list_count);
       if ((r = check_launch("svoo_co_cluster (prune)"))) return r;
@@ -1178,10 +1749,10 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   // the sorted recount runs instead, chosen on the device.
   for (int it = 0; it < max_iters && rc == SVOO_OK; ++it) {
     if ((rc = side(k, k_cent, q_cent, k_labels, k_sizes, k_sorted_idx, k_offsets, sums_k, kc, qc, jpad_k, nch,
-                   it == 0, kPruneKeys, eold_k, delta_k, bnd_k)))
+                   it == 0, kPruneKeys, eold_k, delta_k, bnd_k, key_cand)))
       break;
     if ((rc = side(q, q_cent, k_cent, q_labels, q_sizes, q_sorted_idx, q_offsets, sums_q, qc, kc, jpad_q,
-                   nch + kCounterStride, it == 0, kPruneQueries, eold_q, delta_q, bnd_q)))
+                   nch + kCounterStride, it == 0, kPruneQueries, eold_q, delta_q, bnd_q, false)))
       break;
   }
   // The stable sort of the final labels (the first iteration's sort already is when max_iters == 1).

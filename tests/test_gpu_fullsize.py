@@ -86,6 +86,33 @@ def test_wan_clustering_replays_against_oracle(wan):
     say(wan["name"], "near-tie label differences over", cfg.kmeans_iters, "iterations:", ties)
 
 
+@pytest.mark.parametrize("start", ["random", "warm"])
+def test_wan_key_candidate_pass_changes_nothing(wan, start, monkeypatch):
+    """The key side's candidate pass (exact triangle-inequality pruning in profile space, iterations 2-5) gives
+    bit-identical clustering outputs to full passes, from a random start (many label moves, long candidate lists,
+    recounts) and from a warm start (the benchmark's case)."""
+    from svoo_amd import synth
+    from svoo_amd.co_clustering import co_cluster_tokens_full
+
+    cfg = wan["cfg"]
+    qf, kf = wan["q"][0], wan["k"][0]
+    if start == "random":
+        kw = dict(init_q_idx=wan["qi"], init_k_idx=wan["ki"])
+    else:
+        prev = co_cluster_tokens_full(qf, kf, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters,
+                                      init_q_idx=wan["qi"], init_k_idx=wan["ki"])
+        kw = dict(init_q_centroids=synth.perturb_centroids(cfg, prev["qcentroids"], 3),
+                  init_k_centroids=synth.perturb_centroids(cfg, prev["kcentroids"], 4))
+    res = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("SVOO_KEY_CANDIDATES", flag)
+        say(wan["name"], start, "clustering, key candidate pass", "on" if flag == "1" else "off")
+        res[flag] = co_cluster_tokens_full(qf, kf, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, **kw)
+        torch.cuda.synchronize()
+    for key in res["0"]:
+        assert torch.equal(res["0"][key], res["1"][key]), key
+
+
 def test_wan_block_mask_matches_oracle(wan):
     cfg = wan["cfg"]
     last = wan["separate"][1]

@@ -205,6 +205,44 @@ def test_save_qk_dump(monkeypatch, tmp_path):
     assert torch.equal(d["q"], q) and torch.equal(d["k"], k) and d["timestep"] == 999.0 and d["layer_idx"] == 3
 
 
+def test_candidate_exclusion_bound():
+    """The key-side candidate pass (cocluster.hip) drops cluster j of a token with anchor a when
+    D_aj = |P_a - P_j| >= 2 d_a + m, d_a = |u - P_a|, u = y / |y|.  Its argument: then
+    P_a . y - P_j . y >= |y| (m^2 - nu) / 2 with nu >= max_j n_j - n_a for rows of squared norm n_j <= 1 (the
+    l2norm's eps).  Checked on random profiles with non-unit rows, including the extreme of the bound; a
+    plausible slip (d_a instead of 2 d_a in the radius) is caught by the same data."""
+    rng = np.random.default_rng(11)
+    worst = np.inf
+    slip_caught = False
+    for _ in range(400):
+        kp, J = int(rng.integers(2, 24)), int(rng.integers(2, 96))
+        P = rng.normal(size=(J, kp))
+        P /= np.linalg.norm(P, axis=1, keepdims=True)
+        P *= np.sqrt(1.0 - rng.uniform(0.0, 1e-3, size=J))[:, None]
+        n = (P * P).sum(1)
+        y = rng.normal(size=kp) * rng.uniform(0.01, 100.0)
+        yn = np.linalg.norm(y)
+        a = int(rng.integers(J))
+        # anchors near the token too (the candidate pass's usual case)
+        if rng.random() < 0.5:
+            y = yn * (P[a] + rng.normal(size=kp) * rng.uniform(0.0, 0.5))
+            yn = np.linalg.norm(y)
+        u = y / yn
+        d_a = np.linalg.norm(u - P[a])
+        D = np.linalg.norm(P - P[a], axis=1)
+        nu = n.max() - n[a]
+        m = rng.uniform(0.0, 0.3)
+        excl = D >= 2.0 * d_a + m
+        if excl.any():
+            margin = (P[a] @ y - P[excl] @ y) - yn * (m * m - nu) / 2.0
+            worst = min(worst, margin.min() / yn)
+        slip = (D >= d_a + m) & ~excl
+        if slip.any() and ((P[slip] @ y) > P[a] @ y).any():
+            slip_caught = True
+    assert worst >= -1e-12
+    assert slip_caught
+
+
 def test_dynamic_ratio_from_profile():
     from svoo_amd.sparsity import SparsityLookup
 
