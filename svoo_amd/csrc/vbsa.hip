@@ -735,17 +735,20 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   } else if constexpr (HC) {
     // Half item: local tile u of stream x is global tile 2u + x; stream 0 (n0 tiles) lives in the
     // k_s / v_s buffers and is used by group A, stream 1 (n1 tiles) in k1_s / v1_s, used by group B.
-    // Group B fetches both streams with the full item's timing; waves 4-7 resolve the four tables.
+    // Each group copies its own stream's tiles during its softmax; waves 4-7 resolve the four tables.
     const int n0 = (ntiles + 1) / 2, n1 = ntiles / 2;
-    auto fetch2 = [&](int u, uint16_t* kdst0, uint16_t* vdst0, uint16_t* kdst1, uint16_t* vdst1) __attribute__((always_inline)) {
-      if (u + 2 < n0) dma(kb, rowtab[0][0][u & 1], kdst0);
-      if (u + 1 < n0) dma(vb, rowtab[0][1][(u + 1) & 1], vdst0);
-      if (u + 2 < n1) dma(kb, rowtab[1][0][u & 1], kdst1);
-      if (u + 1 < n1) dma(vb, rowtab[1][1][(u + 1) & 1], vdst1);
+    // Tables of step u (waves 4-7, at the end of group B's softmax half-step): K(u+3) and V(u+2) of each stream.
+    auto resolve2 = [&](int u) __attribute__((always_inline)) {
       if (wave == 4 && u + 3 < n0) resolve(rowtab[0][0][(u + 1) & 1], 2 * (u + 3), 2);
       if (wave == 5 && u + 2 < n0) resolve(rowtab[0][1][u & 1], 2 * (u + 2), 2);
       if (wave == 6 && u + 3 < n1) resolve(rowtab[1][0][(u + 1) & 1], 2 * (u + 3) + 1, 2);
       if (wave == 7 && u + 2 < n1) resolve(rowtab[1][1][u & 1], 2 * (u + 2) + 1, 2);
+    };
+    // Rows of the copies of K(u+2) and V(u+1) of a stream with n tiles (tables of slot u & 1 and (u + 1) & 1).
+    // A tile past the stream takes row 0 of the head: the copy lands in a buffer that is not read for it.
+    auto rows2 = [&](int x, int u, int n, int4& rk, int4& rv) __attribute__((always_inline)) {
+      rk = u + 2 < n ? dma_rows(rowtab[x][0][u & 1]) : make_int4(0, 0, 0, 0);
+      rv = u + 1 < n ? dma_rows(rowtab[x][1][(u + 1) & 1]) : make_int4(0, 0, 0, 0);
     };
     if (wave == 4) {
       resolve(rowtab[0][0][0], 0, 2);
@@ -787,36 +790,53 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     if (wave == 4 && n0 > 2) resolve(rowtab[0][0][0], 4, 2);
     if (wave == 6 && n1 > 2) resolve(rowtab[1][0][0], 5, 2);
     __syncthreads();
-    //   A: h = 2u -> M(u), h = 2u+1 -> V(u+1) on stream 0;  B: h = 2u -> V(u) + fetch, h = 2u+1 -> M(u)
-    //   on stream 1.  Group B runs out of tiles first (n1 <= n0) and then only fetches.
+    //   A: h = 2u -> M(u), h = 2u+1 -> V(u+1) with the copies of stream 0's K(u+2), V(u+1) spread through it;
+    //   B: h = 2u -> V(u) with the copies of stream 1's K(u+2), V(u+1) spread through it and the tables,
+    //   h = 2u+1 -> M(u).  Each group's copies land in buffers the other group does not read, by the barrier
+    //   that ends the half-step; group B runs out of tiles first (n1 <= n0) and then only copies.
     for (int u = 0; u < n0; u += 2) {
+      int4 rk, rv;
       if (!group_b) {
         if (active) mphase(u, v_s0, k_s1);
       } else {
-        fetch2(u, k_s0, v_s1, k1_s0, v1_s1);
-        if (active && u < n1) vphase(2 * u + 1);
+        rows2(1, u, n1, rk, rv);
+        if (active && u < n1)
+          vphase(2 * u + 1, true, rk, k1_s0, rv, v1_s1);
+        else
+          dma_all(rk, k1_s0, rv, v1_s1);
+        resolve2(u);
       }
       __syncthreads();
       if (!group_b) {
-        if (active && u + 1 < n0) vphase(2 * u + 2);
+        rows2(0, u, n0, rk, rv);
+        if (active && u + 1 < n0)
+          vphase(2 * u + 2, true, rk, k_s0, rv, v_s1);
+        else
+          dma_all(rk, k_s0, rv, v_s1);
       } else {
         if (active && u < n1) mphase(u, v1_s0, k1_s1);
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       __syncthreads();
       if (u + 1 >= n0) break;
       if (!group_b) {
         if (active) mphase(u + 1, v_s1, k_s0);
       } else {
-        fetch2(u + 1, k_s1, v_s0, k1_s1, v1_s0);
-        if (active && u + 1 < n1) vphase(2 * u + 3);
+        rows2(1, u + 1, n1, rk, rv);
+        if (active && u + 1 < n1)
+          vphase(2 * u + 3, true, rk, k1_s1, rv, v1_s0);
+        else
+          dma_all(rk, k1_s1, rv, v1_s0);
+        resolve2(u + 1);
       }
       __syncthreads();
       if (!group_b) {
-        if (active && u + 2 < n0) vphase(2 * u + 4);
+        rows2(0, u + 1, n0, rk, rv);
+        if (active && u + 2 < n0)
+          vphase(2 * u + 4, true, rk, k_s1, rv, v_s0);
+        else
+          dma_all(rk, k_s1, rv, v_s0);
       } else {
         if (active && u + 1 < n1) mphase(u + 1, v1_s1, k1_s0);
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       __syncthreads();
     }
