@@ -1015,16 +1015,17 @@ constexpr int kCandTB = 1;                  // token blocks of 32 per wave
 constexpr int kCandWaveTok = 32 * kCandTB;  // label-sorted positions per wave
 constexpr int kCandBlockTok = 4 * kCandWaveTok;
 
-// radius: one wave per kCandWaveTok consecutive positions of the head's label-sorted order.  Writes, per
-// position, the token's anchor and radius (or -1) and the cluster maxima to trad (float bits, zero on entry),
-// one atomic per distinct anchor of a wave.  C is staged in LDS once per block (16-byte chunk c of row r at
-// chunk swz(r, c)).
+// radius: one wave per kCandWaveTok consecutive positions of the head's label-sorted order.  The anchor of a
+// position is pos_anc (the sorted labels of the last sort, moved along by the score kernel's certified
+// labels).  Writes, per position, the radius (or -1) and the cluster maxima to trad (float bits, zero on
+// entry), one atomic per distinct anchor of a wave.  C is staged in LDS once per block (16-byte chunk c of
+// row r at chunk swz(r, c)).
 __global__ void __launch_bounds__(256) cocluster_radius_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ cother, const uint16_t* __restrict__ e_hi,
     const uint16_t* __restrict__ e_lo, const float* __restrict__ nrm, const uint32_t* __restrict__ nu_bits,
     const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max, const int32_t* __restrict__ t_head,
-    const int32_t* __restrict__ sorted_idx, const int32_t* __restrict__ labels, int n, int j, int jpad, int ko,
-    float* __restrict__ pos_t, int32_t* __restrict__ pos_anc, uint32_t* __restrict__ trad) {
+    const int32_t* __restrict__ sorted_idx, const int32_t* __restrict__ pos_anc, int n, int j, int jpad, int ko,
+    float* __restrict__ pos_t, uint32_t* __restrict__ trad) {
   constexpr int TB = kCandTB;
   __shared__ __attribute__((aligned(16))) uint16_t s_c[128 * 128];
   __shared__ float s_cf[4];
@@ -1037,7 +1038,9 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
 #pragma unroll
   for (int cb = 0; cb < TB; ++cb) {
     inpos[cb] = p0 + cb * 32 + l32 < n;
-    tok[cb] = sorted_idx[(size_t)bidx * n + min(p0 + cb * 32 + l32, n - 1)];
+    const size_t o = (size_t)bidx * n + min(p0 + cb * 32 + l32, n - 1);
+    tok[cb] = sorted_idx[o];
+    anc[cb] = pos_anc[o];
   }
   {
     float sq = 0.0f;
@@ -1055,7 +1058,6 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
   }
 #pragma unroll
   for (int cb = 0; cb < TB; ++cb) {
-    anc[cb] = labels[(size_t)bidx * n + tok[cb]];
     vt[cb] = inpos[cb] && anc[cb] >= 0 && anc[cb] < j;
     if (!vt[cb]) anc[cb] = 0;
   }
@@ -1106,11 +1108,7 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
     const float yn = sqrtf(ysq[cb] + __shfl_xor(ysq[cb], 32));
     const float xnu = sqrtf(xn2[cb] * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
     tr[cb] = vt[cb] ? cand_radius(sa[cb], yn, xnu, cfro, emax, nrm[(size_t)bidx * jpad + anc[cb]], nu) : -1.0f;
-    if (inpos[cb] && h == 0) {
-      const size_t o = (size_t)bidx * n + p0 + cb * 32 + l32;
-      pos_t[o] = tr[cb];
-      pos_anc[o] = vt[cb] ? anc[cb] : -1;
-    }
+    if (inpos[cb] && h == 0) pos_t[(size_t)bidx * n + p0 + cb * 32 + l32] = tr[cb];
   }
   // cluster maxima: one atomic per distinct anchor of the wave
   const int myanc = cand_slot<TB>(anc, h, l32);
@@ -1202,14 +1200,14 @@ __global__ void __launch_bounds__(256) cocluster_nu_kernel(const float* __restri
   if (threadIdx.x % kWave == 0) atomicMax(nu_bits + bidx, __float_as_uint(2.0f * dv * (1.0f + 0x1p-20f) + 0x1p-40f));
 }
 
-// score: one wave per kCandWaveTok consecutive label-sorted positions, as in the radius kernel, whose
-// per-position anchors and radii it reads.  The wave's distinct anchors (usually one or two) bring their lists;
+// score: one wave per kCandWaveTok consecutive label-sorted positions, as in the radius kernel: the same
+// anchors, the radii it wrote.  A certified label also becomes the position's anchor for the next pass.  The wave's distinct anchors (usually one or two) bring their lists;
 // the union (a bitmap in the wave's LDS, then compacted in cluster order) is scored on the hi + lo MFMA 32
 // clusters at a time.  One reservation per block and list.
 __global__ void __launch_bounds__(256) cocluster_score_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi, const uint16_t* __restrict__ e_lo,
     const int16_t* __restrict__ lists, const int32_t* __restrict__ list_n, const float* __restrict__ pos_t,
-    const int32_t* __restrict__ pos_anc, const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max,
+    int32_t* __restrict__ pos_anc, const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max,
     const int32_t* __restrict__ t_head, const int32_t* __restrict__ sorted_idx, int32_t* __restrict__ labels, int n,
     int j, int jpad, int2* __restrict__ changes, int32_t* __restrict__ nchanges, int32_t* __restrict__ fb_list,
     int32_t* __restrict__ fb_count) {
@@ -1260,6 +1258,9 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
   }
   u32x4_t xop[TB][8];
   float xn2[TB];
+  int old[TB];  // the token's label before this pass (the anchor unless the fallback kernel moved it)
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) old[cb] = wv ? labels[(size_t)bidx * n + tok[cb]] : 0;
   if (wv) cand_tokens<TB>(x + (size_t)bidx * n * 128, tok, h, xop, xn2);
   // the anchors' lists into the bitmap (a list longer than kCandList leaves its tokens to the fallback)
   __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the bitmap is clear
@@ -1378,7 +1379,7 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
     cert[cb] = vt[cb] && lok[cb] && !uover && fin[cb] && ofin && (best - second) > 2.0f * etok && lab[cb] >= 0;
     const bool mine = inpos[cb] && h == 0;
     fbm[cb] = __ballot(mine && !cert[cb]);
-    chm[cb] = __ballot(mine && cert[cb] && lab[cb] != anc[cb]);
+    chm[cb] = __ballot(mine && cert[cb] && lab[cb] != old[cb]);
     nfb += (int)__popcll(fbm[cb]);
     nch += (int)__popcll(chm[cb]);
   }
@@ -1405,9 +1406,10 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
     const bool mine = inpos[cb] && h == 0;
     if (mine && !cert[cb]) fb_list[(size_t)bidx * n + fbase + mask_rank(fbm[cb])] = tok[cb];
     if (mine && cert[cb]) {
-      if (lab[cb] != anc[cb])
-        changes[cbase + mask_rank(chm[cb])] = make_int2(bidx * n + tok[cb], (anc[cb] << 16) | lab[cb]);
+      if (lab[cb] != old[cb])
+        changes[cbase + mask_rank(chm[cb])] = make_int2(bidx * n + tok[cb], (old[cb] << 16) | lab[cb]);
       labels[(size_t)bidx * n + tok[cb]] = lab[cb];
+      pos_anc[(size_t)bidx * n + p0 + cb * 32 + l32] = lab[cb];
     }
     fbase += (int)__popcll(fbm[cb]);
     cbase += (int)__popcll(chm[cb]);
@@ -1560,16 +1562,17 @@ extern "C" int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, co
 //   delta_k/q    [bh][jpad_k/q] fp32         (per-row change of E since that pass)
 //   bnd_k/q      [3][bh][n] fp32             (per-token pruning bounds of each side)
 //   plist        [bh][n] int32               (tokens the pruning test left to the assignment pass)
-// and for the key side's candidate pass (qc <= 128 only; bnd_k's first two planes hold the radius and the
-// anchor of each label-sorted position):
+// and for the key side's candidate pass (qc <= 128 only; bnd_k's first plane holds the radius of each
+// label-sorted position):
 //   praw_k       [bh][jpad_k][128] bf16      (raw key-centroid profiles)
 //   inv_k        [bh][jpad_k] fp64, nrm_k [bh][jpad_k] fp32   (1 / |praw|, |P|^2)
 //   trad_k       [bh][jpad_k] fp32 bits      (cluster radii)
 //   lists_k      [bh][jpad_k][kCandList] int16, list_n_k [bh][jpad_k] int32   (candidate lists)
+//   kslab        [bh][n] int32               (the key side's sorted labels, the candidate pass's anchors)
 struct CoClusterWs {
   size_t e_off, counts_off, sums_off, slab_off, sums_q_off, changes_off, nchanges_off, e16_off, fb_off, stats_off,
       eold_k_off, eold_q_off, delta_k_off, delta_q_off, bnd_k_off, bnd_q_off, plist_off, praw_off, inv_off, nrm_off,
-      trad_off, lists_off, listn_off, total;
+      trad_off, lists_off, listn_off, kslab_off, total;
 };
 
 static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
@@ -1604,7 +1607,8 @@ static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
   w.trad_off = w.nrm_off + (cand ? al((size_t)bh * jk * sizeof(float)) : 0);
   w.lists_off = w.trad_off + (cand ? al((size_t)bh * jk * sizeof(uint32_t)) : 0);
   w.listn_off = w.lists_off + (cand ? al((size_t)bh * jk * kCandList * sizeof(int16_t)) : 0);
-  w.total = w.listn_off + (cand ? al((size_t)bh * jk * sizeof(int32_t)) : 0);
+  w.kslab_off = w.listn_off + (cand ? al((size_t)bh * jk * sizeof(int32_t)) : 0);
+  w.total = w.kslab_off + (cand ? al((size_t)bh * n * sizeof(int32_t)) : 0);
   return w;
 }
 
@@ -1668,6 +1672,7 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   uint32_t* trad_k = (uint32_t*)(base + lay.trad_off);
   int16_t* lists_k = (int16_t*)(base + lay.lists_off);
   int32_t* listn_k = (int32_t*)(base + lay.listn_off);
+  int32_t* kslab = (int32_t*)(base + lay.kslab_off);
   const bool key_cand = key_candidates_enabled(qc, kc);
   // changed tokens above which an iteration recounts every cluster instead of moving the changed ones
   const int limit = (int)((long long)bh * n / 32);
@@ -1685,6 +1690,9 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
                   int32_t* sorted_idx, int32_t* offsets, double* sums, int kx, int ko, int jpad, int32_t* cnt,
                   bool first, bool prune, double* eold, float* delta, float* bnd, bool cand) -> int {
     int r;
+    // sorted labels of this side's sorts; the key side keeps its own while the candidate pass runs (they are
+    // its anchors)
+    int32_t* sl = cand ? kslab : slab;
     // The certified fp16 pass needs the fp16 copy of E, which the fp64-MFMA prep writes (profile widths up
     // to kPmMaxKp); wider profiles run the hi + lo kernel on every token.
     const bool fp16 = ko <= kPmMaxKp;
@@ -1700,18 +1708,17 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
     int32_t* nc = first ? nullptr : cnt;
     if (cp) {
       const dim3 tgrid((n + kCandBlockTok - 1) / kCandBlockTok, bh);
-      float* pos_t = bnd;                              // plane 0
-      int32_t* pos_anc = (int32_t*)(bnd + (size_t)bh * n);  // plane 1
+      float* pos_t = bnd;  // plane 0
       hipLaunchKernelGGL(cocluster_nu_kernel, dim3(1, bh), dim3(256), 0, s, nrm_k, kx, jpad, nu_bits);
       if ((r = check_launch("svoo_co_cluster (nu)"))) return r;
       if ((r = svoo_zero_i32((int32_t*)trad_k, (long long)bh * jpad, s))) return r;
       hipLaunchKernelGGL(cocluster_radius_kernel, tgrid, dim3(256), 0, s, x, other, e_hi, e_lo, nrm_k, nu_bits, err_max,
-                         norm_max, t_head, sorted_idx, labels, n, kx, jpad, ko, pos_t, pos_anc, trad_k);
+                         norm_max, t_head, sorted_idx, sl, n, kx, jpad, ko, pos_t, trad_k);
       if ((r = check_launch("svoo_co_cluster (radius)"))) return r;
       hipLaunchKernelGGL(cocluster_lists_kernel, dim3(jpad / 32, bh), dim3(256), 0, s, praw_k, inv_k, nrm_k, trad_k, kx,
                          jpad, lists_k, listn_k);
       if ((r = check_launch("svoo_co_cluster (lists)"))) return r;
-      hipLaunchKernelGGL(cocluster_score_kernel, tgrid, dim3(256), 0, s, x, e_hi, e_lo, lists_k, listn_k, pos_t, pos_anc,
+      hipLaunchKernelGGL(cocluster_score_kernel, tgrid, dim3(256), 0, s, x, e_hi, e_lo, lists_k, listn_k, pos_t, sl,
                          err_max, norm_max, t_head, sorted_idx, labels, n, kx, jpad, changes, cnt, fb_list, fb_count);
       if ((r = check_launch("svoo_co_cluster (candidates)"))) return r;
       r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s, changes, cnt, fb_list, fb_count);
@@ -1729,18 +1736,18 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
     }
     if (r) return r;
     if (first) {
-      if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, slab, counts, nullptr, s)))
+      if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, sl, counts, nullptr, s)))
         return r;
-      return svoo_centroid_update_impl(x, sorted_idx, slab, sizes, cent, cent, bh, n, kx, sums, s, 1);
+      return svoo_centroid_update_impl(x, sorted_idx, sl, sizes, cent, cent, bh, n, kx, sums, s, 1);
     }
     // More changed tokens than `limit` (a share of all the tokens at which both updates take about the same
     // time at the Wan shapes): recount every cluster from the sorted labels (guarded kernels, which return at
     // once otherwise); else move the changed tokens.  The choice is made on the device from the count.
     if ((r = svoo_zero_f64_guarded(sums, (long long)bh * kx * 128, cnt, limit, s))) return r;
-    if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, slab, counts, nullptr, s, cnt,
+    if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, sl, counts, nullptr, s, cnt,
                                     limit)))
       return r;
-    svoo_centroid_accumulate_guarded(x, sorted_idx, slab, sums, bh, n, kx, cnt, limit, s);
+    svoo_centroid_accumulate_guarded(x, sorted_idx, sl, sums, bh, n, kx, cnt, limit, s);
     return svoo_centroid_delta_impl(x, changes, cnt, sums, sizes, cent, cent, bh, n, kx, cnt, s, limit);
   };
   // Iteration 1 recounts every cluster from the sorted labels.  Later iterations list the tokens whose label
