@@ -447,11 +447,20 @@ def kernel_table(step, cfg, h, nv, d, qcn, kcn, iters):
         cand = [pz for pz in key_passes[1:] if "cocluster_score_kernel" in pz["k"]]
         full_later = [pz for pz in key_passes[1:] if "cocluster_assign16_kernel" in pz["k"]]
         if cand:
-            avg = lambda names: round(sum(tot(pz, names) for pz in cand) / len(cand), 2)  # noqa: E731
+            # the first candidate pass measures the radii (radius kernel); later ones check each token's radius in
+            # the score kernel against the one its anchor's list was built for
+            def part(pzs, names):
+                return round(sum(tot(pz, names) for pz in pzs) / len(pzs), 2) if pzs else None
+
+            first, later = cand[:1], cand[1:]
             stage["key_candidate_passes"] = {
-                "passes": len(cand), "avg_us": avg(cand_names),
-                "radius_us": avg(("cocluster_radius_kernel",)), "lists_us": avg(("cocluster_lists_kernel",)),
-                "score_us": avg(("cocluster_score_kernel",)), "fallback_us": avg(("cocluster_assign_kernel",)),
+                "passes": len(cand), "avg_us": part(cand, cand_names),
+                "first_pass_us": part(first, cand_names), "later_passes_avg_us": part(later, cand_names),
+                "radius_us": part(first, ("cocluster_radius_kernel",)),
+                "lists_us": part(cand, ("cocluster_lists_kernel",)),
+                "score_first_us": part(first, ("cocluster_score_kernel",)),
+                "score_later_us": part(later, ("cocluster_score_kernel",)),
+                "fallback_us": part(cand, ("cocluster_assign_kernel",)),
                 "note": "iterations 2+: triangle-inequality candidates in profile space, exact (same labels)"}
         if full_later:
             stage["key_full_passes_later_avg_us"] = round(

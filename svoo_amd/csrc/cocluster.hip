@@ -1129,13 +1129,16 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
 
 // lists: one block per 32-row strip of a head; each wave keeps the strip's raw-profile operand and takes every
 // 4th 32-column tile: D_aj^2 >= n_a + n_j - 2 inv_a inv_j (praw_a . praw_j) - 2^-14, and cluster j joins a's
-// list when that is below a's squared radius.  A list that would be longer than kCandList keeps its count.
+// list when that is below a's squared radius (trad * tmul + tadd, also written to tused).  A list that would
+// be longer than kCandList keeps its count.
 __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __restrict__ praw,
                                                               const double* __restrict__ inv,
                                                               const float* __restrict__ nrm,
-                                                              const uint32_t* __restrict__ trad, int j, int jpad,
+                                                              const uint32_t* __restrict__ trad, float tmul,
+                                                              float tadd, int j, int jpad,
                                                               int16_t* __restrict__ lists,
-                                                              int32_t* __restrict__ list_n) {
+                                                              int32_t* __restrict__ list_n,
+                                                              uint32_t* __restrict__ tused) {
   __shared__ int cnt[32];
   __shared__ int16_t lst[32][kCandList];
   const int bidx = blockIdx.y, ta = blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave,
@@ -1156,7 +1159,8 @@ __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __
     const int a = ta * 32 + (r / 4) * 8 + h * 4 + r % 4;
     ia[r] = ib[a];
     na[r] = nb[a];
-    const float t = __uint_as_float(trad[(size_t)bidx * jpad + a]);
+    const float t0 = __uint_as_float(trad[(size_t)bidx * jpad + a]);
+    const float t = t0 > 0.0f ? fmaf(t0, tmul, tadd) : 0.0f;
     th[r] = a < j ? t * t : 0.0f;
   }
   __syncthreads();
@@ -1186,7 +1190,12 @@ __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __
     const int a = ta * 32 + al;
     lists[((size_t)bidx * jpad + a) * kCandList + e] = e < cnt[al] ? lst[al][e] : (int16_t)-1;
   }
-  if (tid < 32) list_n[(size_t)bidx * jpad + ta * 32 + tid] = cnt[tid];
+  if (tid < 32) {
+    const size_t o = (size_t)bidx * jpad + ta * 32 + tid;
+    list_n[o] = cnt[tid];
+    const float t0 = __uint_as_float(trad[o]);
+    tused[o] = __float_as_uint(t0 > 0.0f ? fmaf(t0, tmul, tadd) : 0.0f);  // the radius the list was built for
+  }
 }
 
 // nu of each head: twice the largest |1 - n_a| over its real rows (nu_bits zero on entry).
@@ -1204,19 +1213,40 @@ __global__ void __launch_bounds__(256) cocluster_nu_kernel(const float* __restri
 // anchors, the radii it wrote.  A certified label also becomes the position's anchor for the next pass.  The wave's distinct anchors (usually one or two) bring their lists;
 // the union (a bitmap in the wave's LDS, then compacted in cluster order) is scored on the hi + lo MFMA 32
 // clusters at a time.  One reservation per block and list.
+template <bool SELF>
 __global__ void __launch_bounds__(256) cocluster_score_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi, const uint16_t* __restrict__ e_lo,
     const int16_t* __restrict__ lists, const int32_t* __restrict__ list_n, const float* __restrict__ pos_t,
     int32_t* __restrict__ pos_anc, const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max,
     const int32_t* __restrict__ t_head, const int32_t* __restrict__ sorted_idx, int32_t* __restrict__ labels, int n,
     int j, int jpad, int2* __restrict__ changes, int32_t* __restrict__ nchanges, int32_t* __restrict__ fb_list,
-    int32_t* __restrict__ fb_count) {
+    int32_t* __restrict__ fb_count, const uint16_t* __restrict__ cother, int ko, const float* __restrict__ nrm,
+    const uint32_t* __restrict__ nu_bits, const uint32_t* __restrict__ tused, uint32_t* __restrict__ trec) {
   constexpr int TB = kCandTB;
   __shared__ uint32_t s_bm[4][kCandMaxJ / 32];
   __shared__ int16_t s_u[4][kCandUnion];
   __shared__ int s_cnt[2][4], s_base[2];
+  constexpr int kCRows = SELF ? 128 : 1;
+  __shared__ __attribute__((aligned(16))) uint16_t s_c[kCRows * 128];
+  __shared__ float s_cf[4];
   const int bidx = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, h = lane / 32,
             l32 = lane % 32;
+  if constexpr (SELF) {
+    // C into LDS (16-byte chunk c of row r at chunk swz(r, c)) and ||C||_F, as in the radius kernel
+    const uint16_t* cb_base = cother + (size_t)bidx * ko * 128;
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + 256 * i, r = c / 16, ch = c % 16;
+      const u32x4_t w = r < ko ? ((const u32x4_t*)cb_base)[c] : u32x4_t{0u, 0u, 0u, 0u};
+      *(u32x4_t*)(s_c + r * 128 + swz(r, ch) * 8) = w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sq = dot2_bf16(w[e], w[e], sq);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+    if (lane == 0) s_cf[wave] = sq;
+  }
   const int p0 = blockIdx.x * kCandBlockTok + wave * kCandWaveTok;
   const bool wv = p0 < n;  // the wave has positions (the block's reservations below need every wave)
   uint32_t* bm = s_bm[wave];
@@ -1232,7 +1262,7 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
     const size_t o = (size_t)bidx * n + min(pos, n - 1);
     tok[cb] = sorted_idx[o];
     anc[cb] = pos_anc[o];
-    vt[cb] = inpos[cb] && anc[cb] >= 0 && pos_t[o] > 0.0f;
+    vt[cb] = inpos[cb] && anc[cb] >= 0 && anc[cb] < j && (SELF || pos_t[o] > 0.0f);
     if (!vt[cb]) anc[cb] = 0;
   }
   // distinct anchors: lane k < nd holds the k-th
@@ -1310,13 +1340,14 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
   }
   __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   const bool uover = nu > kCandUnion;
-  float b1[TB], b2[TB];
+  float b1[TB], b2[TB], sav[TB];  // sav: the anchor's score, in the lane that holds its row
   int c1[TB];
   bool fin[TB];
 #pragma unroll
   for (int cb = 0; cb < TB; ++cb) {
     b1[cb] = -INFINITY;
     b2[cb] = -INFINITY;
+    sav[cb] = -INFINITY;
     c1[cb] = -1;
     fin[cb] = true;
   }
@@ -1347,11 +1378,13 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
           const int row = ut * 32 + (r / 4) * 8 + h * 4 + r % 4;
           const float sv = acc[r];
           if (row < nu) {
+            const int cl = ul[row];
             fin[cb] = fin[cb] && (sv > -INFINITY && sv < INFINITY);
+            if (SELF && cl == anc[cb]) sav[cb] = sv;
             if (sv > b1[cb]) {
               b2[cb] = b1[cb];
               b1[cb] = sv;
-              c1[cb] = ul[row];
+              c1[cb] = cl;
             } else if (sv > b2[cb]) {
               b2[cb] = sv;
             }
@@ -1361,6 +1394,61 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
     }
   }
   const float emax = cand_emax(norm_max, err_max, t_head, bidx);
+  // SELF: the token's radius from this pass's y and anchor score must fit in the one its anchor's list was
+  // built for; the radii are recorded (cluster maxima) for the next pass's lists
+  bool rok[TB];
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) rok[cb] = true;
+  if constexpr (SELF) {
+    __syncthreads();  // C is in LDS
+    const float cfro = sqrtf((s_cf[0] + s_cf[1] + s_cf[2] + s_cf[3]) * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
+    const float nu = __uint_as_float(nu_bits[bidx]);
+    float ysq[TB];
+#pragma unroll
+    for (int cb = 0; cb < TB; ++cb) ysq[cb] = 0.0f;
+    if (wv) {
+      for (int ct = 0; ct * 32 < ko; ++ct) {
+        const int crow = ct * 32 + l32;
+        u32x4_t ca[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) ca[ks] = *(const u32x4_t*)(s_c + crow * 128 + swz(crow, ks * 2 + h) * 8);
+#pragma unroll
+        for (int cb = 0; cb < TB; ++cb) {
+          f32x16_t acc = {};
+#pragma unroll
+          for (int ks = 0; ks < 8; ++ks) acc = mfma32x32x16(as_bf16x8(ca[ks]), as_bf16x8(xop[cb][ks]), acc);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) ysq[cb] = fmaf(acc[r], acc[r], ysq[cb]);
+        }
+      }
+    }
+    float tr[TB];
+#pragma unroll
+    for (int cb = 0; cb < TB; ++cb) {
+      const float yn = sqrtf(ysq[cb] + __shfl_xor(ysq[cb], 32));
+      const float sa = fmaxf(sav[cb], __shfl_xor(sav[cb], 32));
+      const float xnu = wv ? sqrtf(xn2[cb] * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f) : 0.0f;
+      tr[cb] = (vt[cb] && sa > -INFINITY) ? cand_radius(sa, yn, xnu, cfro, emax, nrm[(size_t)bidx * jpad + anc[cb]], nu)
+                                          : -1.0f;
+      const float tu = __uint_as_float(tused[(size_t)bidx * jpad + anc[cb]]);
+      rok[cb] = tr[cb] > 0.0f && tr[cb] <= tu;
+    }
+    // record: one atomic per distinct anchor of the wave
+    const int myanc2 = cand_slot<TB>(anc, h, l32);
+    const float myt0 = cand_slot<TB>(tr, h, l32);
+    const float myt = (TB == 1 && h == 1) ? -1.0f : myt0;
+    uint64_t todo2 = __ballot(myt > 0.0f);
+    while (todo2) {
+      const int first = __builtin_ctzll(todo2);
+      const int a = __shfl(myanc2, first);
+      const uint64_t same = __ballot(myt > 0.0f && myanc2 == a);
+      float mx = (same >> lane) & 1 ? myt : 0.0f;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      if (lane == first) atomicMax(trec + (size_t)bidx * jpad + a, __float_as_uint(mx));
+      todo2 &= ~same;
+    }
+  }
   int lab[TB];
   bool cert[TB];
   uint64_t fbm[TB], chm[TB];
@@ -1376,7 +1464,8 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
     const float xnu = wv ? sqrtf(xn2[cb] * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f) : 0.0f;
     const float etok = 0x1p-15f * xnu * emax;
     // b1 == o1 is a tie of two clusters (second == best): not certified
-    cert[cb] = vt[cb] && lok[cb] && !uover && fin[cb] && ofin && (best - second) > 2.0f * etok && lab[cb] >= 0;
+    cert[cb] = vt[cb] && rok[cb] && lok[cb] && !uover && fin[cb] && ofin && (best - second) > 2.0f * etok &&
+               lab[cb] >= 0;
     const bool mine = inpos[cb] && h == 0;
     fbm[cb] = __ballot(mine && !cert[cb]);
     chm[cb] = __ballot(mine && cert[cb] && lab[cb] != old[cb]);
@@ -1516,6 +1605,10 @@ static const bool kPruneKeys = false;
 // whatever the shape (comparisons and tests).
 static const int kCandMaxKp = 128;
 static const int kCandMinKc = 1000;
+// Later candidate passes build each cluster's list for its last measured radius times kCandRadiusGrowth plus
+// kCandRadiusPad (profile space, radii up to 2); a token whose new radius exceeds that goes to the fallback.
+static const float kCandRadiusGrowth = 1.25f;
+static const float kCandRadiusPad = 0.02f;
 static bool key_candidates_enabled(int qc, int kc) {
   if (qc > kCandMaxKp) return false;
   const char* v = getenv("SVOO_KEY_CANDIDATES");
@@ -1569,10 +1662,11 @@ extern "C" int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, co
 //   trad_k       [bh][jpad_k] fp32 bits      (cluster radii)
 //   lists_k      [bh][jpad_k][kCandList] int16, list_n_k [bh][jpad_k] int32   (candidate lists)
 //   kslab        [bh][n] int32               (the key side's sorted labels, the candidate pass's anchors)
+//   trad2_k, tused_k [bh][jpad_k] fp32 bits  (radii recorded by a pass; the radius each list was built for)
 struct CoClusterWs {
   size_t e_off, counts_off, sums_off, slab_off, sums_q_off, changes_off, nchanges_off, e16_off, fb_off, stats_off,
       eold_k_off, eold_q_off, delta_k_off, delta_q_off, bnd_k_off, bnd_q_off, plist_off, praw_off, inv_off, nrm_off,
-      trad_off, lists_off, listn_off, kslab_off, total;
+      trad_off, lists_off, listn_off, kslab_off, trad2_off, tused_off, total;
 };
 
 static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
@@ -1608,7 +1702,9 @@ static CoClusterWs co_cluster_layout(int bh, int n, int qc, int kc) {
   w.lists_off = w.trad_off + (cand ? al((size_t)bh * jk * sizeof(uint32_t)) : 0);
   w.listn_off = w.lists_off + (cand ? al((size_t)bh * jk * kCandList * sizeof(int16_t)) : 0);
   w.kslab_off = w.listn_off + (cand ? al((size_t)bh * jk * sizeof(int32_t)) : 0);
-  w.total = w.kslab_off + (cand ? al((size_t)bh * n * sizeof(int32_t)) : 0);
+  w.trad2_off = w.kslab_off + (cand ? al((size_t)bh * n * sizeof(int32_t)) : 0);
+  w.tused_off = w.trad2_off + (cand ? al((size_t)bh * jk * sizeof(uint32_t)) : 0);
+  w.total = w.tused_off + (cand ? al((size_t)bh * jk * sizeof(uint32_t)) : 0);
   return w;
 }
 
@@ -1673,6 +1769,13 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   int16_t* lists_k = (int16_t*)(base + lay.lists_off);
   int32_t* listn_k = (int32_t*)(base + lay.listn_off);
   int32_t* kslab = (int32_t*)(base + lay.kslab_off);
+  uint32_t* trad2_k = (uint32_t*)(base + lay.trad2_off);
+  uint32_t* tused_k = (uint32_t*)(base + lay.tused_off);
+  // the key side's candidate passes: the first measures the radii (radius kernel); later ones build their lists
+  // from the radii the previous pass recorded, widened by kCandRadiusGrowth
+  int key_cand_pass = 0;
+  uint32_t* t_prev = trad_k;
+  uint32_t* t_rec = trad2_k;
   const bool key_cand = key_candidates_enabled(qc, kc);
   // changed tokens above which an iteration recounts every cluster instead of moving the changed ones
   const int limit = (int)((long long)bh * n / 32);
@@ -1711,15 +1814,28 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
       float* pos_t = bnd;  // plane 0
       hipLaunchKernelGGL(cocluster_nu_kernel, dim3(1, bh), dim3(256), 0, s, nrm_k, kx, jpad, nu_bits);
       if ((r = check_launch("svoo_co_cluster (nu)"))) return r;
-      if ((r = svoo_zero_i32((int32_t*)trad_k, (long long)bh * jpad, s))) return r;
-      hipLaunchKernelGGL(cocluster_radius_kernel, tgrid, dim3(256), 0, s, x, other, e_hi, e_lo, nrm_k, nu_bits, err_max,
-                         norm_max, t_head, sorted_idx, sl, n, kx, jpad, ko, pos_t, trad_k);
-      if ((r = check_launch("svoo_co_cluster (radius)"))) return r;
-      hipLaunchKernelGGL(cocluster_lists_kernel, dim3(jpad / 32, bh), dim3(256), 0, s, praw_k, inv_k, nrm_k, trad_k, kx,
-                         jpad, lists_k, listn_k);
+      const bool measure = key_cand_pass++ == 0;
+      if (measure) {
+        if ((r = svoo_zero_i32((int32_t*)t_prev, (long long)bh * jpad, s))) return r;
+        hipLaunchKernelGGL(cocluster_radius_kernel, tgrid, dim3(256), 0, s, x, other, e_hi, e_lo, nrm_k, nu_bits,
+                           err_max, norm_max, t_head, sorted_idx, sl, n, kx, jpad, ko, pos_t, t_prev);
+        if ((r = check_launch("svoo_co_cluster (radius)"))) return r;
+      }
+      hipLaunchKernelGGL(cocluster_lists_kernel, dim3(jpad / 32, bh), dim3(256), 0, s, praw_k, inv_k, nrm_k, t_prev,
+                         measure ? 1.0f : kCandRadiusGrowth, measure ? 0.0f : kCandRadiusPad, kx, jpad, lists_k,
+                         listn_k, tused_k);
       if ((r = check_launch("svoo_co_cluster (lists)"))) return r;
-      hipLaunchKernelGGL(cocluster_score_kernel, tgrid, dim3(256), 0, s, x, e_hi, e_lo, lists_k, listn_k, pos_t, sl,
-                         err_max, norm_max, t_head, sorted_idx, labels, n, kx, jpad, changes, cnt, fb_list, fb_count);
+      if (measure) {
+        hipLaunchKernelGGL(cocluster_score_kernel<false>, tgrid, dim3(256), 0, s, x, e_hi, e_lo, lists_k, listn_k, pos_t,
+                           sl, err_max, norm_max, t_head, sorted_idx, labels, n, kx, jpad, changes, cnt, fb_list,
+                           fb_count, other, ko, nrm_k, nu_bits, tused_k, t_rec);
+      } else {
+        if ((r = svoo_zero_i32((int32_t*)t_rec, (long long)bh * jpad, s))) return r;
+        hipLaunchKernelGGL(cocluster_score_kernel<true>, tgrid, dim3(256), 0, s, x, e_hi, e_lo, lists_k, listn_k, pos_t,
+                           sl, err_max, norm_max, t_head, sorted_idx, labels, n, kx, jpad, changes, cnt, fb_list,
+                           fb_count, other, ko, nrm_k, nu_bits, tused_k, t_rec);
+        std::swap(t_prev, t_rec);
+      }
       if ((r = check_launch("svoo_co_cluster (candidates)"))) return r;
       r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s, changes, cnt, fb_list, fb_count);
     } else if (pr && !first) {
