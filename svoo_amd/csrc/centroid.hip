@@ -11,9 +11,9 @@
 //   fetched 16 at a time, one batch ahead of the accumulation.
 // finalize: centroid = bf16(f32(sum) / f32(size)), size 0 keeps the old centroid; the sum buffer
 //   is cleared on the way out so the next update starts from zero (or kept, for the delta update).
-// delta: the co-clustering's later iterations move only the rows whose label changed: one wave per
-//   listed token subtracts its row from the old cluster's sums and adds it to the new one's (fp64
-//   atomics) and moves one count.  Under the exponent-span condition above every partial sum is exact,
+// delta: the co-clustering's later iterations move only the rows whose label changed: each wave walks a
+//   piece of the change list, subtracts the rows from their old clusters' sums and adds them to the new
+//   ones' (runs of equal labels summed in registers, then fp64 atomics) and moves the counts.  Under the exponent-span condition above every partial sum is exact,
 //   so the sums equal a full recount bit for bit; beyond it they can differ in the last fp64 bits.
 #include "svoo_common.h"
 
@@ -128,7 +128,14 @@ __global__ void zero_i32_kernel(int32_t* __restrict__ p, long long n) {
   if (i < n) p[i] = 0;
 }
 
-constexpr int kDeltaBlocks = 1024;  // grid-stride over the change list (its length is on the device)
+constexpr int kDeltaBlocks = 1024;  // waves split the change list (its length is on the device) into pieces
+constexpr int kDeltaBatch = 8;      // rows gathered at once per wave
+
+// Each wave takes one contiguous piece of the change list.  The producers write it in runs: a wave of the
+// assignment appends its tokens together, and the key side's candidate pass handles tokens in label order, so
+// neighbouring entries often leave the same cluster or join the same one.  A wave sums a run of equal old (new)
+// labels in registers and adds it with one atomic per element (under the exponent-span condition above every
+// partial sum is exact, so grouping the additions changes nothing).
 __global__ void __launch_bounds__(256) centroid_delta_kernel(const uint32_t* __restrict__ x,
                                                              const int2* __restrict__ changes,
                                                              const int32_t* __restrict__ nchanges,
@@ -139,22 +146,46 @@ __global__ void __launch_bounds__(256) centroid_delta_kernel(const uint32_t* __r
   const int nw = gridDim.x * (blockDim.x / kWave);
   const int total = *nchanges;
   if (total > limit) return;  // the full recount handles this iteration
-  for (int e = w0; e < total; e += nw) {
-    const int2 c = changes[e];
-    const int b = c.x / n, ol = c.y >> 16, nl = c.y & 0xffff;
-    const uint32_t w = x[(size_t)c.x * 64 + lane];
-    const double v0 = (double)bf16_to_f32((uint16_t)(w & 0xffffu)), v1 = (double)bf16_to_f32((uint16_t)(w >> 16));
-    double* sn = sums + ((size_t)b * k + nl) * 128 + 2 * lane;
-    double* so = sums + ((size_t)b * k + ol) * 128 + 2 * lane;
-    atomicAdd(sn, v0);
-    atomicAdd(sn + 1, v1);
-    atomicAdd(so, -v0);
-    atomicAdd(so + 1, -v1);
-    if (lane == 0) {
-      atomicAdd(&sizes[(size_t)b * k + nl], 1);
-      atomicAdd(&sizes[(size_t)b * k + ol], -1);
+  const int per = (total + nw - 1) / nw;
+  const int e0 = w0 * per, e1 = min(total, e0 + per);
+  long long kn = -1, ko = -1;  // cluster rows (head * k + label) of the open runs
+  double n0 = 0.0, n1 = 0.0, o0 = 0.0, o1 = 0.0;
+  int cn = 0, co = 0;
+  auto flush = [&](long long row, double v0, double v1, int cnt) {
+    if (row < 0) return;
+    double* sp = sums + (size_t)row * 128 + 2 * lane;
+    atomicAdd(sp, v0);
+    atomicAdd(sp + 1, v1);
+    if (lane == 0) atomicAdd(&sizes[row], cnt);
+  };
+  for (int e = e0; e < e1; e += kDeltaBatch) {
+    int2 c[kDeltaBatch];
+    uint32_t w[kDeltaBatch];
+#pragma unroll
+    for (int i = 0; i < kDeltaBatch; ++i) c[i] = e + i < e1 ? changes[e + i] : make_int2(-1, 0);
+#pragma unroll
+    for (int i = 0; i < kDeltaBatch; ++i) w[i] = c[i].x >= 0 ? x[(size_t)c[i].x * 64 + lane] : 0u;
+#pragma unroll
+    for (int i = 0; i < kDeltaBatch; ++i) {
+      if (c[i].x < 0) break;  // the same for every lane
+      const long long b = c[i].x / n;
+      const long long rn = b * k + (c[i].y & 0xffff), ro = b * k + (c[i].y >> 16);
+      const double v0 = (double)bf16_to_f32((uint16_t)(w[i] & 0xffffu));
+      const double v1 = (double)bf16_to_f32((uint16_t)(w[i] >> 16));
+      if (rn != kn) {
+        flush(kn, n0, n1, cn);
+        kn = rn, n0 = 0.0, n1 = 0.0, cn = 0;
+      }
+      n0 += v0, n1 += v1, ++cn;
+      if (ro != ko) {
+        flush(ko, o0, o1, co);
+        ko = ro, o0 = 0.0, o1 = 0.0, co = 0;
+      }
+      o0 -= v0, o1 -= v1, --co;
     }
   }
+  flush(kn, n0, n1, cn);
+  flush(ko, o0, o1, co);
 }
 
 }  // namespace svoo

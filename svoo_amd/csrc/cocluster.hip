@@ -162,7 +162,7 @@ __global__ void __launch_bounds__(256) cocluster_prep_kernel(const uint16_t* __r
 //   phase 2: row norms of praw (kept in LDS as bf16, which it is exactly), fp64;
 //   phase 3: E = inv * (praw B) on v_mfma_f32_32x32x16_bf16 (exact products, fp32 sums over the profile
 //            width; fp64 on the 16x16x4 MFMA cost as much as phase 1 again), with B staged through LDS in
-//            64-row chunks of 144-element rows.
+//            64-row chunks of 144-element rows, each requested from memory two chunks ahead.
 constexpr int kPmRows = 16;
 constexpr int kPmChunk = 64;
 constexpr int kPmChunkStride = 144;
@@ -212,19 +212,37 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
   const uint16_t* ab = a + (size_t)bidx * j * 128;
   const uint16_t* bb = bmat + (size_t)bidx * kp * 128;
 
-  // Phase 1.  Rows past j repeat row j - 1 (padding rows of E), columns past kp are zero.
+  // Phase 3's B chunks of 64 rows: this thread's four 16-byte pieces (rows tid / 16 + 16 i, piece tid % 16).
+  // The first two are requested here, before phase 1, and each later one two chunks ahead of its use.
+  auto chunk_load = [&](u32x4_t(&r)[4], int c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r[i] = *((const u32x4_t*)(bb + (size_t)min(c + tid / 16 + 16 * i, kp - 1) * 128) + tid % 16);
+  };
+  u32x4_t pre0[4], pre1[4];
+  chunk_load(pre0, 0);
+  if (kPmChunk < kpp) chunk_load(pre1, kPmChunk);
+
+  // Phase 1.  Rows past j repeat row j - 1 (padding rows of E), columns past kp are zero.  The B rows of the
+  // wave's next column tile are requested before the MFMAs of the current one.
   u32x4_t afr[4];
   {
     const u32x4_t* src = (const u32x4_t*)(ab + (size_t)min(r0 + li, j - 1) * 128) + 4 * q;
 #pragma unroll
     for (int t = 0; t < 4; ++t) afr[t] = src[t];
   }
-  for (int ct = wave; ct < kpp / 16; ct += 4) {
-    const int col = ct * 16 + li;
-    u32x4_t bfr[4];
-    const u32x4_t* bsrc = (const u32x4_t*)(bb + (size_t)min(col, kp - 1) * 128) + 4 * q;
+  auto tile_load = [&](u32x4_t(&r)[4], int ct) {
+    const u32x4_t* bsrc = (const u32x4_t*)(bb + (size_t)min(ct * 16 + li, kp - 1) * 128) + 4 * q;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) bfr[t] = bsrc[t];
+    for (int t = 0; t < 4; ++t) r[t] = bsrc[t];
+  };
+  const int ntile = kpp / 16;
+  u32x4_t bfr[4];
+  if (wave < ntile) tile_load(bfr, wave);
+  for (int ct = wave; ct < ntile; ct += 4) {
+    const int col = ct * 16 + li;
+    u32x4_t bnx[4];
+    if (ct + 4 < ntile) tile_load(bnx, ct + 4);
     f64x4_t acc = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int st = 0; st < 32; ++st) {
@@ -234,6 +252,10 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
 #pragma unroll
     for (int v = 0; v < 4; ++v)  // D row 4 v + q, column li
       praw[(4 * v + q) * ps + col] = col < kp ? f32_to_bf16((float)acc[v]) : (uint16_t)0;
+    if (ct + 4 < ntile) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) bfr[t] = bnx[t];
+    }
   }
   __syncthreads();
 
@@ -285,15 +307,16 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
   const int toff = (8 * (grp / 2) + s16 / 4) * kPmChunkStride + dd0 + 16 * (grp % 2) + 4 * (s16 % 4);
   const int poff = (lane % 16) * ps + 8 * (lane / 32);
   uint32_t bmax = 0;  // max |B| as bf16 magnitude bits (they order like the values)
-  for (int c = 0; c < kpp; c += kPmChunk) {
+  // Stage the chunk held in r (rows c ..), request chunk c + 2 * kPmChunk into r, then the chunk's MFMAs.
+  auto chunk_step = [&](u32x4_t(&r)[4], int c) {
     __syncthreads();  // the previous chunk is consumed
-    for (int t = tid; t < kPmChunk * 16; t += 256) {
-      const int row = t / 16, piece = t % 16;
-      const u32x4_t w = *((const u32x4_t*)(bb + (size_t)min(c + row, kp - 1) * 128) + piece);
-      *(u32x4_t*)(bch + row * kPmChunkStride + piece * 8) = w;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) bmax = max(bmax, max(w[e] & 0x7fffu, (w[e] >> 16) & 0x7fffu));
+    for (int i = 0; i < 4; ++i) {
+      *(u32x4_t*)(bch + (tid / 16 + 16 * i) * kPmChunkStride + (tid % 16) * 8) = r[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bmax = max(bmax, max(r[i][e] & 0x7fffu, (r[i][e] >> 16) & 0x7fffu));
     }
+    if (c + 2 * kPmChunk < kpp) chunk_load(r, c + 2 * kPmChunk);
     __syncthreads();
 #pragma unroll
     for (int st = 0; st < kPmChunk / 16; ++st) {
@@ -304,6 +327,10 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
       const u32x4_t pr = *(const u32x4_t*)(praw + poff + c + 16 * st);
       acc3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(bt), as_bf16x8(pr), acc3, 0, 0, 0);
     }
+  };
+  for (int c = 0; c < kpp; c += 2 * kPmChunk) {
+    chunk_step(pre0, c);
+    if (c + kPmChunk < kpp) chunk_step(pre1, c + kPmChunk);
   }
   uint16_t* hb = e_hi + (size_t)bidx * jpad * 128;
   uint16_t* lb = e_lo + (size_t)bidx * jpad * 128;
@@ -1607,8 +1634,10 @@ static const int kCandMaxKp = 128;
 static const int kCandMinKc = 1000;
 // Later candidate passes build each cluster's list for its last measured radius times kCandRadiusGrowth plus
 // kCandRadiusPad (profile space, radii up to 2); a token whose new radius exceeds that goes to the fallback.
-static const float kCandRadiusGrowth = 1.25f;
-static const float kCandRadiusPad = 0.02f;
+// Measured at C3 (warm start): 1.05 / 0.005 and 1.1 / 0 leave as many tokens to the fallback as the measuring
+// pass does; 1.25 / 0.02 leaves about 10% more (longer lists overflow), 1.5 / 0.04 five times more.
+static const float kCandRadiusGrowth = 1.05f;
+static const float kCandRadiusPad = 0.005f;
 static bool key_candidates_enabled(int qc, int kc) {
   if (qc > kCandMaxKp) return false;
   const char* v = getenv("SVOO_KEY_CANDIDATES");
