@@ -1165,7 +1165,8 @@ __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __
                                                               float tadd, int j, int jpad,
                                                               int16_t* __restrict__ lists,
                                                               int32_t* __restrict__ list_n,
-                                                              uint32_t* __restrict__ tused) {
+                                                              uint32_t* __restrict__ tused,
+                                                              uint32_t* __restrict__ tzero) {
   __shared__ int cnt[32];
   __shared__ int16_t lst[32][kCandList];
   const int bidx = blockIdx.y, ta = blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave,
@@ -1222,6 +1223,7 @@ __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __
     list_n[o] = cnt[tid];
     const float t0 = __uint_as_float(trad[o]);
     tused[o] = __float_as_uint(t0 > 0.0f ? fmaf(t0, tmul, tadd) : 0.0f);  // the radius the list was built for
+    if (tzero) tzero[o] = 0u;  // the radii the score kernel is about to record
   }
 }
 
@@ -1841,6 +1843,7 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
     if (cp) {
       const dim3 tgrid((n + kCandBlockTok - 1) / kCandBlockTok, bh);
       float* pos_t = bnd;  // plane 0
+      // nu in a launch of its own: from the prep's blocks, 10^4 atomics on one word per head cost ~50 us
       hipLaunchKernelGGL(cocluster_nu_kernel, dim3(1, bh), dim3(256), 0, s, nrm_k, kx, jpad, nu_bits);
       if ((r = check_launch("svoo_co_cluster (nu)"))) return r;
       const bool measure = key_cand_pass++ == 0;
@@ -1852,14 +1855,13 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
       }
       hipLaunchKernelGGL(cocluster_lists_kernel, dim3(jpad / 32, bh), dim3(256), 0, s, praw_k, inv_k, nrm_k, t_prev,
                          measure ? 1.0f : kCandRadiusGrowth, measure ? 0.0f : kCandRadiusPad, kx, jpad, lists_k,
-                         listn_k, tused_k);
+                         listn_k, tused_k, measure ? nullptr : t_rec);
       if ((r = check_launch("svoo_co_cluster (lists)"))) return r;
       if (measure) {
         hipLaunchKernelGGL(cocluster_score_kernel<false>, tgrid, dim3(256), 0, s, x, e_hi, e_lo, lists_k, listn_k, pos_t,
                            sl, err_max, norm_max, t_head, sorted_idx, labels, n, kx, jpad, changes, cnt, fb_list,
                            fb_count, other, ko, nrm_k, nu_bits, tused_k, t_rec);
       } else {
-        if ((r = svoo_zero_i32((int32_t*)t_rec, (long long)bh * jpad, s))) return r;
         hipLaunchKernelGGL(cocluster_score_kernel<true>, tgrid, dim3(256), 0, s, x, e_hi, e_lo, lists_k, listn_k, pos_t,
                            sl, err_max, norm_max, t_head, sorted_idx, labels, n, kx, jpad, changes, cnt, fb_list,
                            fb_count, other, ko, nrm_k, nu_bits, tused_k, t_rec);
