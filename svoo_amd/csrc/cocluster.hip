@@ -723,13 +723,9 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
     top2[cb] = -INFINITY;
     tbase[cb] = 0;
   }
-  // +inf the optimiser cannot see (a visible one folds med3(x, t, +inf) back into a max with NaN quieting)
-  uint32_t pinf_bits;
-  __asm__ volatile("s_mov_b32 %0, 0x7f800000" : "=s"(pinf_bits));
-  const float pinf = __uint_as_float(pinf_bits);
   f32x16_t acc[4];
-  // Top-two update of token block cb with tile jb: per score a tag, a median of three and a max (written as a
-  // median with +inf: fmaxf on bit-cast values would add a NaN-quieting instruction per score).
+  // Top-two update of token block cb with tile jb: per score a tag, a median of three and a max (the IEEE
+  // maximum builtin: fmaxf on bit-cast values would add a NaN-quieting instruction per score).
   auto epi = [&](int cb, int jb) __attribute__((always_inline)) {
     const float prev = top1[cb];
 #pragma unroll
