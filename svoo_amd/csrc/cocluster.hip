@@ -1625,8 +1625,8 @@ static const bool kPruneKeys = false;
 // The key side's candidate pass (radius, lists and score kernels) replaces the full pass from the second
 // iteration on when the query centroids fit one 128-row operand and there are at least kCandMinKc key clusters.
 // Its cost hardly depends on the cluster count while the full pass's grows with it; measured at the Wan shapes
-// (same labels either way): 500 key clusters, 1.29 ms full against 1.44 ms with it per 5-iteration clustering;
-// 1000 key clusters, 6.47 against 6.29 ms.  SVOO_KEY_CANDIDATES=0 / 1 in the environment switches it off / on
+// (same labels either way, warm start): 500 key clusters, 1.31 ms full against 1.39 ms with it per 5-iteration
+// clustering; 1000 key clusters, 6.4-6.5 against 5.6 ms.  SVOO_KEY_CANDIDATES=0 / 1 in the environment switches it off / on
 // whatever the shape (comparisons and tests).
 static const int kCandMaxKp = 128;
 static const int kCandMinKc = 1000;
