@@ -1188,11 +1188,17 @@ __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __
     th[r] = a < j ? t * t : 0.0f;
   }
   __syncthreads();
-  for (int tj = wave; tj < nt; tj += 4) {
+  // the wave's column tiles tj = wave, wave + 4, ...; the next tile's rows are requested before this one's MFMAs
+  auto tile_load = [&](u32x4_t(&r)[8], int tj) __attribute__((always_inline)) {
     const u32x4_t* brow = (const u32x4_t*)(pb + (size_t)(tj * 32 + l32) * 128);
-    u32x4_t bop[8];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) bop[ks] = brow[ks * 2 + h];
+    for (int ks = 0; ks < 8; ++ks) r[ks] = brow[ks * 2 + h];
+  };
+  u32x4_t bop[8];
+  if (wave < nt) tile_load(bop, wave);
+  for (int tj = wave; tj < nt; tj += 4) {
+    u32x4_t bnx[8];
+    if (tj + 4 < nt) tile_load(bnx, tj + 4);
     f32x16_t acc = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) acc = mfma32x32x16(as_bf16x8(aop[ks]), as_bf16x8(bop[ks]), acc);
@@ -1206,6 +1212,10 @@ __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __
         const int slot = atomicAdd(&cnt[al], 1);
         if (slot < kCandList) lst[al][slot] = (int16_t)jj;
       }
+    }
+    if (tj + 4 < nt) {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) bop[ks] = bnx[ks];
     }
   }
   __syncthreads();
