@@ -1630,8 +1630,14 @@ static const int kMaxClusters = 4096;
 // Pruning per side.  Measured on the C3 workload (one head, warm start, exact scores on the CPU): from the
 // second iteration on the test settles 95-99% of the query tokens (100 clusters) and 4-8% of the key tokens
 // (1000 clusters, whose top-two gaps are small against the centroid moves).
-static const bool kPruneQueries = true;
+// SVOO_QUERY_PRUNE=0 in the environment switches the query side's pruning off (comparisons and tests).  A pruned
+// token keeps its label, which is then the exact argmax of x.E; an unpruned pass gives the hi + lo kernel's label,
+// which can differ from the exact argmax only where two scores lie within that kernel's rounding.
 static const bool kPruneKeys = false;
+static bool query_prune_enabled() {
+  const char* v = getenv("SVOO_QUERY_PRUNE");
+  return !(v && v[0] == '0' && v[1] == 0);
+}
 // The key side's candidate pass (radius, lists and score kernels) replaces the full pass from the second
 // iteration on when the query centroids fit one 128-row operand and there are at least kCandMinKc key clusters.
 // Its cost hardly depends on the cluster count while the full pass's grows with it; measured at the Wan shapes
@@ -1814,6 +1820,7 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   uint32_t* t_prev = trad_k;
   uint32_t* t_rec = trad2_k;
   const bool key_cand = key_candidates_enabled(qc, kc);
+  const bool prune_q = query_prune_enabled();
   // changed tokens above which an iteration recounts every cluster instead of moving the changed ones
   const int limit = (int)((long long)bh * n / 32);
   const int jpad_k = pad_to(kc, kAssignChunk), jpad_q = pad_to(qc, kAssignChunk);
@@ -1912,7 +1919,7 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
                    it == 0, kPruneKeys, eold_k, delta_k, bnd_k, key_cand)))
       break;
     if ((rc = side(q, q_cent, k_cent, q_labels, q_sizes, q_sorted_idx, q_offsets, sums_q, qc, kc, jpad_q,
-                   nch + kCounterStride, it == 0, kPruneQueries, eold_q, delta_q, bnd_q, false)))
+                   nch + kCounterStride, it == 0, prune_q, eold_q, delta_q, bnd_q, false)))
       break;
   }
   // The stable sort of the final labels (the first iteration's sort already is when max_iters == 1).

@@ -139,6 +139,7 @@ __global__ void __launch_bounds__(kEarThreads) ear_logits_kernel(const uint16_t*
 // in both operands, so every lane loads 128 contiguous bytes of its row.
 constexpr int kEffClusters = 8;
 constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
+constexpr double kInvSqrtD = 0.08838834764831845;  // 128^-1/2
 
 // expm1(x) for |x| <= 0.1 by its Taylor series to x^4 (truncation below 1e-6 relative); beyond
 // 0.1 the difference e^a - e^c itself loses at most 6e-8 / 0.1 relative in fp32.
@@ -178,12 +179,36 @@ __global__ void __launch_bounds__(kEarThreads) ear_efficiency_kernel(
       const float c2 = c * kLog2e;
       // sums of e^2 |u|^2, e d (u . vc) and d^2, relative to the running max m2 (log2 units)
       float m2 = c2, sd = 0.0f, sg = 0.0f, sc = 0.0f;
+      // A one-member cluster's key centroid is its member (a mean of one value is exact) and u = 0, so its error
+      // d^2 |vc|^2 is set by x = a - c alone, which is the bf16 rounding of the logit: an fp32 dot (~1e-6
+      // absolute) would leave x wrong by percents.  Every lane then loads the member's row and also forms
+      // qc_i . k exactly in fp64 (bf16 products are exact there).
+      const bool single = cnt == 1;
+      float x_single = 0.0f;
       for (int tt = 0; tt < cnt; tt += 32) {
-        const int row = min(start + tt + l32, n - 1);
+        const int row = single ? start : min(start + tt + l32, n - 1);
         const u32x4_t* kr = (const u32x4_t*)(kb + (size_t)row * 128) + 8 * h;
         u32x4_t ka[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) ka[s] = kr[s];
+        if (single) {
+          // operands re-read from memory (L1/L2 hits) in a rolled loop: fp64 copies of the register-resident
+          // operands would be hoisted out of the cluster loop and cost 128 VGPRs
+          const u32x4_t* qsrc = (const u32x4_t*)(qc + ((size_t)b * qn + ic) * 128) + 8 * h;
+          double dot = 0.0;
+#pragma unroll 1
+          for (int s = 0; s < 8; ++s) {
+            const u32x4_t qw = qsrc[s], kw = kr[s];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const double q0 = bf16_to_f32((uint16_t)(qw[e] & 0xffffu)), q1 = bf16_to_f32((uint16_t)(qw[e] >> 16));
+              const double k0 = bf16_to_f32((uint16_t)(kw[e] & 0xffffu)), k1 = bf16_to_f32((uint16_t)(kw[e] >> 16));
+              dot = fma(q1, k1, fma(q0, k0, dot));
+            }
+          }
+          dot += __shfl_xor(dot, 32);
+          x_single = (float)(dot * kInvSqrtD - (double)c);
+        }
         // token statistics of this lane's 16 tokens, loaded with the K rows (clamped rows are masked below)
         float2 sv[16];
 #pragma unroll
@@ -213,7 +238,7 @@ __global__ void __launch_bounds__(kEarThreads) ear_efficiency_kernel(
         for (int r = 0; r < 16; ++r) {
           const int tok = tt + (r / 4) * 8 + h * 4 + (r % 4);
           const float e = __builtin_amdgcn_exp2f(av[r] - m2);  // 0 for masked tokens
-          const float x = (av[r] - c2) * kLn2;                  // a_t - c_ij
+          const float x = single ? x_single : (av[r] - c2) * kLn2;  // a_t - c_ij
           float d = fabsf(x) <= kExpm1Lim ? pc * expm1_small(x) : e - pc;
           if (!full && tok >= cnt) d = 0.0f;
           sd = fmaf(e * e, sv[r].x, sd);

@@ -57,7 +57,11 @@ def _query_chunk_rows(query: torch.Tensor, key: torch.Tensor) -> int:
     """
     b, h, rows_q, _ = query.shape
     bytes_per_row = max(1, b * h * key.size(2) * _SCORE_BYTES)
-    free = torch.cuda.mem_get_info(query.device)[0]
+    try:
+        free = torch.cuda.mem_get_info(query.device)[0]
+    except Exception:
+        # No free-memory figure (the query itself failed): a small fixed chunk, as the reference falls back to.
+        return int(min(128, rows_q))
     budget = min(_MAX_CHUNK_SCORE_BYTES, int(free * _memory_share()))
     rows = budget // bytes_per_row
     if rows >= 64:
@@ -155,35 +159,63 @@ def compute_exact_attention_sparsity(
 
 
 def resume_requested() -> bool:
-    """``SVOO_SPARSITY_RESUME`` set to a true value (1, true, yes, on; any case) turns the resume guard on."""
-    return os.environ.get("SVOO_SPARSITY_RESUME", "").strip().lower() in {"1", "true", "yes", "on"}
+    """The resume guard is on unless ``SVOO_SPARSITY_RESUME`` is unset or one of ``0``, the empty string,
+    ``false`` and ``False`` (``svoo/sparsity/exact.py:50-51``, ``svoo/models/wan/inference.py:334``): any
+    other value keeps the raw log and skips what it already holds."""
+    return os.environ.get("SVOO_SPARSITY_RESUME", "0") not in ("0", "", "false", "False")
 
 
 class SparsityLogIndex:
     """The (layer, step) -> heads entries of one raw sparsity log.
 
-    The log is parsed once, when the guard first asks about it (a resumed run sees what the interrupted
-    one wrote); afterwards the index learns this process's own appends through :meth:`add`, so a long
-    profiling run never re-reads the growing file.  Entries another process appends to the same file
-    after the first read are not seen.
+    Each query stats the file: when its identity (device, inode) changed or it shrank below what was read,
+    the index is rebuilt from the start; when it grew, only the new complete lines are parsed (the reference's
+    cache, ``svoo/sparsity/exact.py:54-102``).  An unterminated last line is left for a later read, so a
+    line being written is never taken in half.  :meth:`add` records this process's own appends at once.
     """
 
     def __init__(self, path: str):
         self.path = path
         self.heads: Dict[Tuple[int, int], Set[int]] = {}
-        entry = None
+        self._file_id = None
+        self._offset = 0
+        self._entry = None
+        self.refresh()
+
+    def _reset(self, file_id) -> None:
+        self.heads = {}
+        self._file_id = file_id
+        self._offset = 0
+        self._entry = None
+
+    def refresh(self) -> None:
+        """Bring the index up to the file's current contents."""
         try:
-            with open(path, "r", encoding="utf-8") as f:
-                for line in f:
-                    m = _SPARSITY_HEADER_RE.match(line)
-                    if m:
-                        entry = self.heads.setdefault((int(m.group(1)), int(m.group(2))), set())
-                    elif entry is not None:
-                        hm = _SPARSITY_HEAD_RE.match(line)
-                        if hm:
-                            entry.add(int(hm.group(1)))
+            st = os.stat(self.path)
         except OSError:
-            pass
+            return
+        file_id = (st.st_dev, st.st_ino)
+        if file_id != self._file_id or st.st_size < self._offset:
+            self._reset(file_id)
+        if st.st_size == self._offset:
+            return
+        try:
+            with open(self.path, "rb") as f:
+                f.seek(self._offset)
+                data = f.read()
+        except OSError:
+            return
+        end = data.rfind(b"\n") + 1
+        for raw in data[:end].splitlines():
+            line = raw.decode("utf-8", errors="replace")
+            m = _SPARSITY_HEADER_RE.match(line)
+            if m:
+                self._entry = self.heads.setdefault((int(m.group(1)), int(m.group(2))), set())
+            elif self._entry is not None:
+                hm = _SPARSITY_HEAD_RE.match(line)
+                if hm:
+                    self._entry.add(int(hm.group(1)))
+        self._offset += end
 
     def add(self, layer_idx: int, step: int, heads) -> None:
         self.heads.setdefault((int(layer_idx), int(step)), set()).update(int(h) for h in heads)
@@ -208,7 +240,9 @@ def has_completed_sparsity_entry(output_file: str, layer_idx: int, step: int, nu
     this layer/step, so the measurement can be skipped (``svoo/sparsity/exact.py:54-102``)."""
     if not resume_requested() or not output_file or not os.path.exists(output_file):
         return False
-    return _log_index(output_file).complete(layer_idx, step, num_heads)
+    index = _log_index(output_file)
+    index.refresh()
+    return index.complete(layer_idx, step, num_heads)
 
 
 def record_sparsity_entry(output_file: str, layer_idx: int, step: int, heads) -> None:

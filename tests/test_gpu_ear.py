@@ -130,6 +130,39 @@ def test_efficiency_matches_oracle(gpu, h, s, qn, kn, gamma, qscale, seed):
     np.testing.assert_allclose(got, want, rtol=0, atol=EFF_ABS)
 
 
+def test_efficiency_of_one_member_clusters(gpu):
+    """A one-member cluster's key centroid is its member and its value centroid its value, so the error is
+    ``(pc expm1(a - c))^2 |vc|^2`` with ``a - c`` the bf16 rounding of the logit: the score must carry the exact
+    ``a``, not an fp32 dot's (which moves the log error by percents)."""
+    from svoo_amd import ear
+
+    say("ear efficiency, one-member clusters")
+    r = np.random.default_rng(21)
+    h, qn, kn = 2, 64, 200
+    ks = np.ones((h, kn), np.int32)
+    ks[:, ::7] = r.integers(2, 40, size=ks[:, ::7].shape)  # a few larger clusters among the singletons
+    s = int(ks.sum(1).max())
+    ks[:, -1] += s - ks.sum(1)
+    qs = rand_sizes(r, h, qn, s)
+    kp, kpt = rand_bf16((1, h, s, 128), 22, gpu, 1.0)
+    vp, vpt = rand_bf16((1, h, s, 128), 23, gpu, 1.0)
+    qc, qct = rand_bf16((1, h, qn, 128), 24, gpu, 1.0)
+    kst, qst = _i32(ks[None], gpu), _i32(qs[None], gpu)
+    vc = ear.value_centroids_from_permuted(vpt, kst)
+    # key centroids as the clustering leaves them: the member mean, which is the member itself for one member
+    kc = np.zeros((1, h, kn, 128), np.float32)
+    for b in range(h):
+        off = np.concatenate([[0], np.cumsum(ks[b])])
+        for j in range(kn):
+            kc[0, b, j] = O.bf16_round(kp[0, b, off[j]:off[j + 1]].mean(0).astype(np.float32))
+    kct = bf16(kc, gpu)
+    c = ear.centroid_logits(qct, kct)
+    eff = ear.error_estimation_triton(qct, kct, vc, kpt, vpt, qst, kst, c, 1.0, 1e-8)
+    torch.cuda.synchronize()
+    want = O.ear_efficiency_scores(qc[0], f32(c)[0], kp[0], vp[0], f32(vc)[0], qs, ks, 1.0)[None]
+    np.testing.assert_allclose(f32(eff), want, rtol=0, atol=EFF_ABS)
+
+
 # ------------------------------------------------------------------------------------------ selection
 @pytest.mark.parametrize("kn", [7, 256, 300, 1000, 2100])
 @pytest.mark.parametrize("top_p,ratio", [(0.9, 0.0), (0.5, 0.1), (1.0, [0.05, 0.3]), (0.7, [0.2])])

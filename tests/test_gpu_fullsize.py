@@ -11,6 +11,11 @@ half-step against the oracle on the GPU's own inputs (labels up to near-ties, ce
 mask equals the oracle's on the same centroids (bit-exact); the fused and separate paths give identical bits;
 sampled output rows equal a float64 softmax over exactly the keys the mask keeps (bf16 tolerance).  C3 also
 checks the permute round trip and the dense one-cluster map against torch's bf16 attention.
+
+Each shape runs in two mask modes: density mode (top_p 0, the per-head profile ratio as the minimum) and the
+mode the reference's Wan launchers ship (top_p 0.9, the profile ratios clipped to [0.15, 0.20];
+scripts/inference/wan/wan_t2v_720p_svoo.sh:77-84 and :98-105).  The clustering does not depend on the mode, so
+the clustering-only checks run in density mode.
 """
 
 import numpy as np
@@ -24,7 +29,23 @@ from parity_helpers import (MAX_ABS, MIN_COS, check_clustering, replay_clusterin
 pytestmark = pytest.mark.gpu
 
 
-def _wan_calls(cfg, gpu, q, k, v, qi, ki, rho):
+TOP_P_SHIPPED = 0.9
+RATIO_CLIP = (0.15, 0.20)
+
+
+def mask_mode(mode, rho):
+    """``(top_p, per-head minimum ratios)`` of a mask mode."""
+    if mode == "density":
+        return 0.0, rho
+    return TOP_P_SHIPPED, [min(max(r, RATIO_CLIP[0]), RATIO_CLIP[1]) for r in rho]
+
+
+def density_only(case):
+    if case["mode"] != "density":
+        pytest.skip("the clustering does not depend on the mask mode; checked in density mode")
+
+
+def _wan_calls(cfg, gpu, q, k, v, qi, ki, top_p, ratios):
     from svoo_amd.processor import WanAttn_SAPAttn_Processor
 
     res = {}
@@ -34,12 +55,12 @@ def _wan_calls(cfg, gpu, q, k, v, qi, ki, rho):
 
         P.num_frame, P.frame_size, P.context_length = cfg.frames, cfg.frame_size, 0
         P.num_q_centroids, P.num_k_centroids = cfg.num_q_centroids, cfg.num_k_centroids
-        P.top_p_kmeans, P.min_kc_ratio, P.max_kc_ratio = 0.0, rho, 0
+        P.top_p_kmeans, P.min_kc_ratio, P.max_kc_ratio = top_p, ratios, 0
         P.kmeans_iter_init = P.kmeans_iter_step = cfg.kmeans_iters
         P.first_times_fp, P.first_layers_fp = float("inf"), 0
         P.kmeans_init_idx = (qi, ki)
         P.fuse_permutes = fused
-        say(cfg.name, "processor call,", "fused" if fused else "separate permutes")
+        say(cfg.name, "processor call, top_p", top_p, "fused" if fused else "separate permutes")
         proc = P(layer_idx=0)
         out = proc.attention_core_logic(q, k, v, None)
         torch.cuda.synchronize()
@@ -47,18 +68,22 @@ def _wan_calls(cfg, gpu, q, k, v, qi, ki, rho):
     return res
 
 
-@pytest.fixture(scope="module", params=["C2", "C3"])
+@pytest.fixture(scope="module", params=["C2", "C3", "C2-topp", "C3-topp"])
 def wan(request, gpu):
     from svoo_amd import synth
 
-    cfg = synth.CONFIGS[request.param]
-    say(cfg.name, "inputs", cfg.heads, cfg.tokens)
+    name, _, mode = request.param.partition("-")
+    mode = mode or "density"
+    cfg = synth.CONFIGS[name]
+    say(cfg.name, "inputs", cfg.heads, cfg.tokens, "mask mode", mode)
     q, k, v = synth.make_qkv_device(cfg, gpu)
     qi = synth.init_indices(cfg, cfg.heads, cfg.num_q_centroids, cfg.tokens, 1).to(gpu)
     ki = synth.init_indices(cfg, cfg.heads, cfg.num_k_centroids, cfg.tokens, 2).to(gpu)
     rho = synth.head_densities(cfg)
-    res = _wan_calls(cfg, gpu, q, k, v, qi, ki, rho)
-    yield dict(name=request.param, cfg=cfg, q=q, k=k, v=v, qi=qi, ki=ki, rho=rho, **res)
+    top_p, ratios = mask_mode(mode, rho)
+    res = _wan_calls(cfg, gpu, q, k, v, qi, ki, top_p, ratios)
+    yield dict(name=name, mode=mode, cfg=cfg, q=q, k=k, v=v, qi=qi, ki=ki, rho=rho, top_p=top_p, ratios=ratios,
+               **res)
     del res, q, k, v
     torch.cuda.empty_cache()
 
@@ -78,6 +103,7 @@ def test_wan_clustering_replays_against_oracle(wan):
     """Head 0, every half-step of the 5 iterations: labels vs the literal argmin (near-ties excepted), key
     centroids and query centroids bit-exact against an exact recount (iterations 2-5 are the incremental
     update), and the last state equal to the processor's clustering of that head."""
+    density_only(wan)
     cfg = wan["cfg"]
     r = wan["separate"][1]["clustering"]
     head0 = {key: r[key][:1] for key in ("qlabels", "klabels", "qcentroids", "kcentroids", "qsizes", "ksizes")}
@@ -91,6 +117,7 @@ def test_wan_key_candidate_pass_changes_nothing(wan, start, monkeypatch):
     """The key side's candidate pass (exact triangle-inequality pruning in profile space, iterations 2-5) gives
     bit-identical clustering outputs to full passes, from a random start (many label moves, long candidate lists,
     recounts) and from a warm start (the benchmark's case)."""
+    density_only(wan)
     from svoo_amd import synth
     from svoo_amd.co_clustering import co_cluster_tokens_full
 
@@ -113,16 +140,45 @@ def test_wan_key_candidate_pass_changes_nothing(wan, start, monkeypatch):
         assert torch.equal(res["0"][key], res["1"][key]), key
 
 
+@pytest.mark.parametrize("start", ["random", "warm"])
+def test_wan_query_pruning_changes_nothing(wan, start, monkeypatch):
+    """The query side's pruning of later passes (tokens whose bounds prove their label cannot change are
+    skipped) gives the same clustering outputs as unpruned passes.  A pruned token keeps the exact argmax of x.E;
+    an unpruned one gets the certified fp16 label or the hi + lo kernel's, which equal the exact argmax except
+    where two scores lie within the hi + lo rounding, and a pruned token's bounds separate its scores by more."""
+    density_only(wan)
+    from svoo_amd import synth
+    from svoo_amd.co_clustering import co_cluster_tokens_full
+
+    cfg = wan["cfg"]
+    qf, kf = wan["q"][0], wan["k"][0]
+    if start == "random":
+        kw = dict(init_q_idx=wan["qi"], init_k_idx=wan["ki"])
+    else:
+        prev = co_cluster_tokens_full(qf, kf, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters,
+                                      init_q_idx=wan["qi"], init_k_idx=wan["ki"])
+        kw = dict(init_q_centroids=synth.perturb_centroids(cfg, prev["qcentroids"], 3),
+                  init_k_centroids=synth.perturb_centroids(cfg, prev["kcentroids"], 4))
+    res = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("SVOO_QUERY_PRUNE", flag)
+        say(wan["name"], start, "clustering, query pruning", "on" if flag == "1" else "off")
+        res[flag] = co_cluster_tokens_full(qf, kf, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, **kw)
+        torch.cuda.synchronize()
+    for key in res["0"]:
+        assert torch.equal(res["0"][key], res["1"][key]), key
+
+
 def test_wan_block_mask_matches_oracle(wan):
     cfg = wan["cfg"]
     last = wan["separate"][1]
     r = last["clustering"]
-    say(wan["name"], "block mask vs oracle")
+    say(wan["name"], wan["mode"], "block mask vs oracle")
     h, d = cfg.heads, cfg.head_dim
     qc = r["qcentroids"].float().cpu().numpy().reshape(1, h, cfg.num_q_centroids, d)
     kc = r["kcentroids"].float().cpu().numpy().reshape(1, h, cfg.num_k_centroids, d)
-    om, olens = O.identify_dynamic_map(qc, kc, last["q_sizes"].cpu().numpy(), last["k_sizes"].cpu().numpy(), 0.0,
-                                       wan["rho"], 0, return_lengths=True)
+    om, olens = O.identify_dynamic_map(qc, kc, last["q_sizes"].cpu().numpy(), last["k_sizes"].cpu().numpy(),
+                                       wan["top_p"], wan["ratios"], 0, return_lengths=True)
     np.testing.assert_array_equal(last["map"].cpu().numpy(), om)
     np.testing.assert_array_equal(last["lengths"].cpu().numpy(), olens)
 
@@ -149,8 +205,8 @@ def test_wan_sampled_rows_match_float64(wan, path):
 def test_c3_permute_round_trip(wan):
     from svoo_amd.permute import apply_inverse_permutation, permute_pair_by_indices
 
-    if wan["name"] != "C3":
-        pytest.skip("C3 only")
+    if wan["name"] != "C3" or wan["mode"] != "density":
+        pytest.skip("C3 density case only (the check does not depend on the mask mode)")
     say("C3 permute / inverse permute round trip")
     k, v = wan["k"], wan["v"]
     order = wan["separate"][1]["clustering"]["k_sorted_idx"]
@@ -168,8 +224,8 @@ def test_c3_dense_mask_equals_sdpa(wan):
 
     from svoo_amd.co_clustering import dynamic_block_sparse_fwd
 
-    if wan["name"] != "C3":
-        pytest.skip("C3 only")
+    if wan["name"] != "C3" or wan["mode"] != "density":
+        pytest.skip("C3 density case only (the check does not depend on the mask mode)")
     cfg = wan["cfg"]
     h, n = cfg.heads, cfg.tokens
     say("C3 dense mask vs torch bf16 attention")
@@ -187,18 +243,20 @@ def test_c3_dense_mask_equals_sdpa(wan):
 
 
 # ------------------------------------------------------------------------------------------ C4 (HunyuanVideo)
-@pytest.fixture(scope="module")
-def c4(gpu):
+@pytest.fixture(scope="module", params=["density", "topp"])
+def c4(request, gpu):
     from svoo_amd import synth
     from svoo_amd.processor import Hunyuan_SAPAttn_Processor
 
+    mode = request.param
     cfg = synth.CONFIGS["C4"]
-    say(cfg.name, "inputs", cfg.heads, cfg.tokens)
+    say(cfg.name, "inputs", cfg.heads, cfg.tokens, "mask mode", mode)
     q, k, v = synth.make_qkv_device(cfg, gpu)
     nv = cfg.video_tokens
     qi = synth.init_indices(cfg, cfg.heads, cfg.num_q_centroids, nv, 1).to(gpu)
     ki = synth.init_indices(cfg, cfg.heads, cfg.num_k_centroids, nv, 2).to(gpu)
     rho = synth.head_densities(cfg)
+    top_p, ratios = mask_mode(mode, rho)
     res = {}
     for prompt in (cfg.text_tokens, 200):  # whole text as prompt (empty padding cluster); 56 padding tokens
         for fused in (False, True):
@@ -208,17 +266,18 @@ def c4(gpu):
             P.num_frame, P.frame_size, P.context_length = cfg.frames, cfg.frame_size, cfg.text_tokens
             P.prompt_length = prompt
             P.num_q_centroids, P.num_k_centroids = cfg.num_q_centroids, cfg.num_k_centroids
-            P.top_p_kmeans, P.min_kc_ratio, P.max_kc_ratio = 0.0, rho, 0
+            P.top_p_kmeans, P.min_kc_ratio, P.max_kc_ratio = top_p, ratios, 0
             P.kmeans_iter_init = P.kmeans_iter_step = cfg.kmeans_iters
             P.first_times_fp, P.first_layers_fp = float("inf"), 0
             P.kmeans_init_idx = (qi, ki)
             P.fuse_permutes = fused
-            say(cfg.name, "processor call, prompt", prompt, "fused" if fused else "separate permutes")
+            say(cfg.name, "processor call, prompt", prompt, "top_p", top_p,
+                "fused" if fused else "separate permutes")
             proc = P(layer_idx=0)
             out = proc.attention_core_logic(q, k, v, 0.0, 0)
             torch.cuda.synchronize()
             res[(prompt, fused)] = (out.contiguous(), proc._last_call)
-    yield dict(cfg=cfg, q=q, k=k, v=v, qi=qi, ki=ki, rho=rho, res=res)
+    yield dict(cfg=cfg, mode=mode, q=q, k=k, v=v, qi=qi, ki=ki, rho=rho, top_p=top_p, ratios=ratios, res=res)
     del res, q, k, v
     torch.cuda.empty_cache()
 
@@ -242,13 +301,13 @@ def test_c4_clustering_and_masks_match_oracle(c4):
     for prompt in (256, 200):
         last = c4["res"][(prompt, True)][1]
         r = last["clustering"]
-        say("C4 clustering and masks vs oracle, prompt", prompt)
+        say("C4", c4["mode"], "clustering and masks vs oracle, prompt", prompt)
         check_clustering(r["qlabels"], r["qsizes"], r["q_sorted_idx"], r["q_offsets"], qn)
         check_clustering(r["klabels"], r["ksizes"], r["k_sorted_idx"], r["k_offsets"], kn)
         qs, ks = r["qsizes"].cpu().numpy().reshape(1, h, qn), r["ksizes"].cpu().numpy().reshape(1, h, kn)
         om, olens = O.identify_dynamic_map(r["qcentroids"].float().cpu().numpy().reshape(1, h, qn, d),
-                                           r["kcentroids"].float().cpu().numpy().reshape(1, h, kn, d), qs, ks, 0.0,
-                                           c4["rho"], 0, return_lengths=True)
+                                           r["kcentroids"].float().cpu().numpy().reshape(1, h, kn, d), qs, ks,
+                                           c4["top_p"], c4["ratios"], 0, return_lengths=True)
         np.testing.assert_array_equal(last["video_lengths"].cpu().numpy(), olens)
         m2, qs2, ks2, qidx2 = O.hunyuan_post_process(om, qs, ks, r["q_sorted_idx"].cpu().numpy(), nv, ctx, prompt)
         _, _, _, kidx2 = O.hunyuan_post_process(om, qs, ks, r["k_sorted_idx"].cpu().numpy(), nv, ctx, prompt)
@@ -261,6 +320,7 @@ def test_c4_clustering_and_masks_match_oracle(c4):
 
 def test_c4_clustering_replays_against_oracle(c4):
     """Head 0 of the video part, every half-step of the 5 iterations, ending in the processor's clustering."""
+    density_only(c4)
     cfg = c4["cfg"]
     nv = cfg.video_tokens
     r = c4["res"][(256, True)][1]["clustering"]

@@ -490,9 +490,12 @@ def test_sparsity_resume_guard(tmp_path, monkeypatch):
     log.write_text("\n".join(format_sparsity_log(3, "self", 7, 0.95, 0.1, [0.1] * 4, 50, 50)) + "\n")
     monkeypatch.delenv("SVOO_SPARSITY_RESUME", raising=False)
     assert not has_completed_sparsity_entry(str(log), 3, 7, 4)  # opt-in only
-    for off in ("0", "false", "no", ""):
+    for off in ("0", "false", "False", ""):  # the reference's off values (svoo/sparsity/exact.py:50-51)
         monkeypatch.setenv("SVOO_SPARSITY_RESUME", off)
         assert not has_completed_sparsity_entry(str(log), 3, 7, 4)
+    for on in ("2", "y", "enabled", "FALSE", "no"):  # any other value is on there, so it is here
+        monkeypatch.setenv("SVOO_SPARSITY_RESUME", on)
+        assert has_completed_sparsity_entry(str(log), 3, 7, 4), on
     monkeypatch.setenv("SVOO_SPARSITY_RESUME", "True")
     assert has_completed_sparsity_entry(str(log), 3, 7, 4)
     assert not has_completed_sparsity_entry(str(log), 3, 7, 5)
@@ -510,6 +513,25 @@ def test_sparsity_resume_guard(tmp_path, monkeypatch):
     assert exact.SparsityLogIndex(str(part)).complete(0, 2, 2)
     assert not exact.SparsityLogIndex(str(part)).complete(0, 2, 3)
     assert not exact.SparsityLogIndex(str(tmp_path / "absent.txt")).complete(0, 1, 1)
+    # another writer's appends are read on the next query; an unterminated line waits for its newline
+    lines = format_sparsity_log(5, "self", 1, 0.95, 0.1, [0.1] * 2, 50, 50)
+    with open(log, "a") as f:
+        f.write("\n".join(lines[:2]) + "\n" + lines[2][:9])
+    assert not has_completed_sparsity_entry(str(log), 5, 1, 2)
+    with open(log, "a") as f:
+        f.write(lines[2][9:] + "\n")
+    assert has_completed_sparsity_entry(str(log), 5, 1, 2)
+    # a truncated or replaced log is read again from the start: its old entries are gone
+    log.write_text("\n".join(format_sparsity_log(9, "self", 1, 0.95, 0.1, [0.1], 50, 50)) + "\n")
+    assert not has_completed_sparsity_entry(str(log), 3, 7, 4)
+    assert has_completed_sparsity_entry(str(log), 9, 1, 1)
+    repl = tmp_path / "raw_new.txt"
+    repl.write_text("\n".join(format_sparsity_log(3, "self", 7, 0.95, 0.1, [0.1] * 4, 50, 50)) + "\n" * 40)
+    import os
+
+    os.replace(repl, log)  # same path, new inode, larger file
+    assert has_completed_sparsity_entry(str(log), 3, 7, 4)
+    assert not has_completed_sparsity_entry(str(log), 9, 1, 1)
 
 
 def test_sparsity_chunk_rows_and_oom_backoff(monkeypatch):
@@ -533,6 +555,13 @@ def test_sparsity_chunk_rows_and_oom_backoff(monkeypatch):
     assert exact._query_chunk_rows(q, k) == 5000  # the 4 GiB cap holds 357913 rows: all 5000 fit
     q_long = torch.zeros(1, 2, 10 ** 6, 128)
     assert exact._query_chunk_rows(q_long, k) == ((4 << 30) // per_row) // 64 * 64
+
+    def no_info(dev=None):
+        raise RuntimeError("hipMemGetInfo failed")
+
+    monkeypatch.setattr(torch.cuda, "mem_get_info", no_info)
+    assert exact._query_chunk_rows(q, k) == 128  # the reference's fallback, min(128, rows)
+    assert exact._query_chunk_rows(q[:, :, :50], k) == 50
 
     # the loop, with the score GEMM's output on the CPU and a count stand-in (no device here)
     calls = []

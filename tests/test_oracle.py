@@ -10,9 +10,13 @@ Pinning map (oracle function -> independent checks):
   profile_centroids           unit rows; bf16-rounded matmul entries
   cocluster_assign            brute force with math.fsum; reduced form argmax x.E; K == 1
   co_cluster_tokens           well-separated mixture recovered exactly; fixed point of the update
+  centroid_scores             hand-computed bf16 values of bf16(Qc.Kc^T) * fl32(1/sqrt(D)) for integer
+                              dots that bf16 cannot hold; torch's CPU bf16 matmul and scalar division
   weighted_softmax            scipy softmax (unit weights); closed form w / sum(w) for equal scores
   identify_dynamic_map        p >= 1 all-true; p = 0 keeps max(1, int(r*Kc)); hand-computed top-p
-                              cut; prefix property; top-1 kept; float32 ratio semantics (0.7 -> 699)
+                              cut; prefix property; top-1 kept; float32 ratio semantics (0.7 -> 699);
+                              a hand-worked row whose kept set at p = 0.9 changes if the dot is not
+                              rounded to bf16 or the scale is 1/D
   kv_plan_indices             brute force on a hand-made map
   block_sparse_attention      dense SDPA (torch, float64) for an all-true map; block-diagonal map;
                               empty row -> 0
@@ -269,6 +273,59 @@ def test_mask_hand_computed_top_p():
     # ties 0 and 4 (both 1/16): stable order keeps j=0 before j=4 at p = 0.9
     m = O.identify_dynamic_map(qc, kc, qs, ks, 0.0, min_kc_ratio=0.8)[0, 0, 0]
     assert np.nonzero(m)[0].tolist() == [0, 1, 2, 3]
+
+
+def _int_row(a, b, e):
+    v = np.zeros(128, np.float32)
+    v[:3] = (a, b, e)
+    return v
+
+
+def test_centroid_scores_hand_computed():
+    # svoo/co_clustering.py:578: bf16 matmul, then "/ (D ** 0.5)" on the bf16 result.
+    # q = (16, 16, 1, 0, ...), so q.k = 16*k0 + 16*k1 + k2, exact small integers.
+    # bf16 keeps 8 significant bits: in [1024, 2048) its spacing is 8, in [256, 512) it is 2.
+    # fl32(1/sqrt(128)) = fl32(1 / fl32(11.3137...)) = 0.088388346; in [64, 128) bf16's spacing is 0.5,
+    # in [16, 32) 0.125.
+    #   dot 1027 -> bf16 1024 -> 1024 * 0.088388346 = 90.5097 -> bf16 90.5
+    #        (unrounded dot: 1027 * 0.0883883 = 90.775 -> 91.0; scaled by 1/128: 8.0)
+    #   dot 1029 -> bf16 1032 -> 91.2168 -> 91.0  (unrounded: 90.952 -> 91.0)
+    #   dot 1032 -> bf16 1032 -> 91.0
+    #   dot  257 -> bf16 256 (tie, even mantissa) -> 22.6274 -> bf16 22.625 (unrounded: 22.7158 -> 22.75)
+    #   dot -1027 -> -90.5
+    #   dot    5 -> 0.441942 -> bf16 0.44140625 (= 113/256)
+    q = _int_row(16, 16, 1)
+    keys = [_int_row(32, 32, 3), _int_row(32, 32, 5), _int_row(32, 32, 8), _int_row(8, 8, 1),
+            _int_row(-32, -32, -3), _int_row(0, 0, 5)]
+    qc = q[None, None, None, :]
+    kc = np.stack(keys)[None, None]
+    expect = np.array([90.5, 91.0, 91.0, 22.625, -90.5, 0.44140625], np.float32)
+    np.testing.assert_array_equal(O.centroid_scores(qc, kc)[0, 0, 0], expect)
+    # torch's own bf16 matmul and scalar division on the CPU give the same values.
+    tq = torch.from_numpy(qc).bfloat16()
+    tk = torch.from_numpy(kc).bfloat16()
+    ref = (torch.matmul(tq, tk.transpose(-2, -1)) / (128 ** 0.5)).float().numpy()
+    np.testing.assert_array_equal(ref[0, 0, 0], expect)
+
+
+def test_mask_kept_set_depends_on_score_rounding_and_scale():
+    # Key clusters j0, j1, jT with dots 1027, 1029, 1032 (scores 90.5, 91.0, 91.0 as above) and sizes 3, 2, 24.
+    # Weighted masses in units of e^91: jT 24, j1 2, j0 3 e^-0.5 = 1.8196; total 27.8196.
+    #   sorted: jT 0.8627 (bf16 0.86328125 <= bf16(0.9) = 0.8984375), j1 0.0719, j0 0.0654
+    #   prefix after jT = 0.863 <= 0.898: keep j1; prefix after j1 = 0.935 > 0.898: drop j0  => {j1, jT}
+    # Without the rounding of the dot j0 scores 91.0: masses 24, 3, 2 -> order jT, j0, j1 => {j0, jT}.
+    # With 1/D for 1/sqrt(D) the scores are 8.0, 8.0625, 8.0625: masses 24, 2, 3 e^-0.0625 = 2.818
+    #   -> order jT, j0, j1 => {j0, jT}.
+    q = _int_row(16, 16, 1)
+    kc = np.stack([_int_row(32, 32, 3), _int_row(32, 32, 5), _int_row(32, 32, 8)])[None, None]
+    qc = q[None, None, None, :]
+    ks = np.array([[[3, 2, 24]]], np.int32)
+    m = O.identify_dynamic_map(qc, kc, np.ones((1, 1, 1), np.int32), ks, 0.9)[0, 0, 0]
+    assert m.tolist() == [False, True, True]
+    t = O.centroid_scores(qc, kc)
+    pb = O.weighted_softmax(t, np.broadcast_to(ks[:, :, None, :].astype(np.float64), t.shape))[0, 0, 0]
+    # bf16 of 1.8196/27.8196 = 0.06541, 2/27.8196 = 0.07189, 24/27.8196 = 0.86270 (spacing 2^-11 below 0.125)
+    np.testing.assert_array_equal(pb, np.array([134 / 2048, 147 / 2048, 221 / 256], np.float32))
 
 
 def test_mask_row_params_float32_ratio_semantics():
