@@ -112,16 +112,28 @@ int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int n, int d, 
                     int32_t* k_offsets, void* workspace, size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Scaled centroid scores: scores[bh][i][j] = bf16(bf16(qc_i . kc_j) * f32(1 / sqrt(D))), with
+ * bf16(exact dot) as a bf16 matmul output (rounded through fp32); qc [BH][QN][D], kc [BH][KN][D] bf16.
+ * Replaces the attn_scores of identify_dynamic_map, svoo/co_clustering.py:578
+ * (torch.matmul(query_centroids, key_centroids.transpose(-2, -1)) / D**0.5).
+ * ------------------------------------------------------------------------------------------- */
+int svoo_centroid_scores(const uint16_t* qc, const uint16_t* kc, int bh, int qn, int kn, int d, uint16_t* scores,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Block mask: per (b, h, q-cluster) row, weighted softmax of the scaled centroid scores, stable
  * descending sort, top-p with per-head minimum keep and optional cap, scattered back to a bool map.
  *   preserve[h], cap[h]: per-head counts computed on the host from min_kc_ratio / max_kc_ratio
- *   (cap 0 = none); p_storage: top_p rounded to the storage dtype; full != 0 gives an all-true map.
+ *   (cap 0 = none); p_storage: top_p rounded to the storage dtype; full != 0 gives an all-true map
+ *   (qc, kc, k_sizes, preserve, cap and scores may then be NULL).
  *   map[b][h][i][j] (uint8 0/1), lengths[b][h][i] = kept key clusters (may be NULL).
+ *   scores: [B*H][QN][KN] bf16 buffer of the caller that receives the scaled centroid scores
+ *   (svoo_centroid_scores) from which the mask is built.
  * Replaces weighted_softmax + identify_dynamic_map, svoo/co_clustering.py:544-633.
  * ------------------------------------------------------------------------------------------- */
 int svoo_block_mask(const uint16_t* qc, const uint16_t* kc, const int32_t* k_sizes, const int32_t* preserve,
                     const int32_t* cap, int b, int h, int qn, int kn, int d, float p_storage, int full, uint8_t* map,
-                    int32_t* lengths, void* stream);
+                    int32_t* lengths, uint16_t* scores, void* stream);
 
 /* Weighted softmax of bf16 scores [rows][cols] with fp32 weights (row stride weight_row_stride, 0 = one
  * row shared by all) -> bf16 probabilities.
@@ -181,7 +193,8 @@ int svoo_vbsa_fused_fwd_noalloc(const uint16_t* q, const uint16_t* k, const uint
  *     {|u_t|^2, u_t . v_cent_j} (fp32 pairs, [BH][N][2]; the reference keeps |v_t|^2 and v_cent_j . v_t,
  *     from which these follow).  Replaces _compute_value_centroids (svoo/models/wan/attention.py:593-610)
  *     and _precompute_v_stats_kernel (svoo/co_clustering.py:1315-1396).
- *   svoo_ear_centroid_logits: c[b][i][j] = bf16(bf16(qc_i . kc_j) * D^-0.5), exact dot.
+ *   svoo_ear_centroid_logits: c[b][i][j] = bf16(bf16(qc_i . kc_j) * D^-0.5), exact dot (the same
+ *     values as svoo_centroid_scores).
  *     Replaces the einsum of svoo/co_clustering.py:1725.
  *   svoo_ear_efficiency: eff[b][i][j] = log(max(err_ij, eps)) - gamma log(max(|Q_i||K_j|, eps)) with
  *     err_ij = sum_t || e^{a_t} v_t - e^{c_ij} vc_j ||^2 over the tokens of key cluster j,

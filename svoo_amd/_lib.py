@@ -34,7 +34,8 @@ _SIGS = {
     "svoo_co_cluster_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "svoo_co_cluster": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, c_int,
                                 P, P, P, P, P, P, P, P, P, P, P, c_size_t, P]),
-    "svoo_block_mask": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_int, P, P, P]),
+    "svoo_centroid_scores": (c_int, [P, P, c_int, c_int, c_int, c_int, P, P]),
+    "svoo_block_mask": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_int, P, P, P, P]),
     "svoo_weighted_softmax": (c_int, [P, P, c_longlong, P, c_longlong, c_int, P]),
     "svoo_vbsa_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "svoo_vbsa_fwd": (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_size_t, P, P]),

@@ -315,17 +315,34 @@ def block_mask_lengths(query_centroids, key_centroids, q_cluster_sizes, k_cluste
     full = p >= 1.0
     if full:
         _lib.call("svoo_block_mask", None, None, None, None, None, b, h, qn, kn, d, 0.0, 1, dmap.data_ptr(),
-                  lengths.data_ptr(), _lib.stream_of(dev))
+                  lengths.data_ptr(), None, _lib.stream_of(dev))
         return dmap, lengths
     if qc.dtype != torch.bfloat16 or kc.dtype != torch.bfloat16:
         raise TypeError("identify_dynamic_map: the MI355X path takes bfloat16 centroids")
     preserve, cap = mask_row_params(h, kn, min_kc_ratio, max_kc_ratio)
     pc = torch.tensor(preserve + cap, dtype=torch.int32).to(dev, non_blocking=True)
     ks = k_cluster_sizes.to(device=dev, dtype=torch.int32).reshape(b * h, kn).contiguous()
+    scores = torch.empty(b, h, qn, kn, dtype=torch.bfloat16, device=dev)
     _lib.call("svoo_block_mask", qc.contiguous().data_ptr(), kc.contiguous().data_ptr(), ks.data_ptr(),
               pc.data_ptr(), pc[h:].data_ptr(), b, h, qn, kn, d, _bf16_value(p), 0, dmap.data_ptr(),
-              lengths.data_ptr(), _lib.stream_of(dev))
+              lengths.data_ptr(), scores.data_ptr(), _lib.stream_of(dev))
     return dmap, lengths
+
+
+def centroid_scores(query_centroids, key_centroids) -> torch.Tensor:
+    """Scaled centroid attention scores ``matmul(Qc, Kc^T) / D**0.5`` of the block mask on bf16 centroids
+    (``svoo/co_clustering.py:578``): the exact dot rounded to bf16, times ``float32(1 / sqrt(D))``, rounded to
+    bf16.  ``[B, H, Qc, D]`` x ``[B, H, Kc, D]`` -> ``[B, H, Qc, Kc]`` bf16."""
+    qc, kc = query_centroids, key_centroids
+    _lib.require_gpu_tensor(qc, "query_centroids")
+    if qc.dtype != torch.bfloat16 or kc.dtype != torch.bfloat16:
+        raise TypeError("centroid_scores: the MI355X path takes bfloat16 centroids")
+    b, h, qn, d = qc.shape
+    kn = kc.shape[2]
+    out = torch.empty(b, h, qn, kn, dtype=torch.bfloat16, device=qc.device)
+    _lib.call("svoo_centroid_scores", qc.contiguous().data_ptr(), kc.contiguous().data_ptr(), b * h, qn, kn, d,
+              out.data_ptr(), _lib.stream_of(qc.device))
+    return out
 
 
 def identify_dynamic_map(query_centroids, key_centroids, q_cluster_sizes, k_cluster_sizes, p, min_kc_ratio=0,

@@ -4,7 +4,7 @@
 // Kernels, in call order (all inputs cluster-contiguous, i.e. already permuted):
 //   ear_value_kernel       one block per (bh, key cluster): value centroid vc_j (exact member sum),
 //                          |vc_j|^2 and per token u_t = v_t - vc_j as {|u_t|^2, u_t . vc_j}
-//   ear_logits_kernel      one block per (bh, query cluster): c_ij = bf16(bf16(qc_i . kc_j) * D^-0.5)
+//   (centroid logits)      c_ij = bf16(bf16(qc_i . kc_j) * D^-0.5): svoo_centroid_scores (mask.hip)
 //   ear_efficiency_kernel  MFMA over (32 query centroids x 32 tokens) tiles; per (i, j) the error
 //                          err = sum_t || e_t v_t - pc vc_j ||^2,  e_t = e^{a_t - m},  pc = e^{c_ij - m},
 //                          a_t = qc_i . k_t / sqrt(D), m = max(c_ij, max_t a_t) (online), then
@@ -101,32 +101,6 @@ __global__ void __launch_bounds__(kEarThreads) ear_value_kernel(const uint16_t* 
       cd += __shfl_xor(cd, o);
     }
     if (t < cnt && ch == 0) tok_stats[(size_t)b * n + start + t] = make_float2(vn, cd);
-  }
-}
-
-// ------------------------------------------------------------------------------------------ centroid logits
-__global__ void __launch_bounds__(kEarThreads) ear_logits_kernel(const uint16_t* __restrict__ qc,
-                                                                 const uint16_t* __restrict__ kc, int qn, int kn,
-                                                                 float inv_sqrt_d, uint16_t* __restrict__ c) {
-  __shared__ double qrow[128];
-  const int i = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-  if (tid < 128) qrow[tid] = (double)bf16_to_f32(qc[((size_t)b * qn + i) * 128 + tid]);
-  __syncthreads();
-  const uint16_t* kb = kc + (size_t)b * kn * 128;
-  uint16_t* crow = c + ((size_t)b * qn + i) * kn;
-  for (int j = tid; j < kn; j += kEarThreads) {
-    const u32x4_t* row = (const u32x4_t*)(kb + (size_t)j * 128);
-    double acc = 0.0;
-#pragma unroll 2
-    for (int ch = 0; ch < 16; ++ch) {
-      const u32x4_t w = row[ch];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        acc = fma(qrow[ch * 8 + 2 * e], (double)bf16_to_f32((uint16_t)(w[e] & 0xffffu)), acc);
-        acc = fma(qrow[ch * 8 + 2 * e + 1], (double)bf16_to_f32((uint16_t)(w[e] >> 16)), acc);
-      }
-    }
-    crow[j] = f32_to_bf16(bf16_round_f32((float)acc) * inv_sqrt_d);
   }
 }
 
@@ -448,10 +422,8 @@ extern "C" int svoo_ear_centroid_logits(const uint16_t* qc, const uint16_t* kc, 
   SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_ear_centroid_logits: D=%d (only 128 supported)", d);
   SVOO_REQUIRE(bh > 0 && qn > 0 && kn > 0 && bh <= 65535 && qn <= 65535, SVOO_ERR_INVALID_ARG,
                "svoo_ear_centroid_logits: bad dims");
-  const float inv = 1.0f / (float)sqrt((double)d);
-  hipLaunchKernelGGL(ear_logits_kernel, dim3(qn, bh), dim3(kEarThreads), 0, (hipStream_t)stream, qc, kc, qn, kn, inv,
-                     c_logits);
-  return check_launch("svoo_ear_centroid_logits");
+  // c_ij = bf16(bf16(qc_i . kc_j) * f32(D^-1/2)): the centroid scores of the block mask
+  return svoo_centroid_scores(qc, kc, bh, qn, kn, d, c_logits, stream);
 }
 
 extern "C" int svoo_ear_efficiency(const uint16_t* qc, const uint16_t* k_perm, const uint16_t* c_logits,

@@ -232,6 +232,47 @@ def test_block_mask_bit_exact(gpu, p, mn, mx, qn, kn):
     np.testing.assert_array_equal(lens.cpu().numpy(), olens)
 
 
+def _score_cases():
+    """(name, qc, kc) float32 arrays of bf16 values [1, H, n, 128] for the centroid-score kernel."""
+    r = np.random.default_rng(77)
+    cases = []
+    for scale in (0.05, 0.5, 30.0):
+        qc = O.bf16_round((r.standard_normal((1, 3, 100, 128)) * scale).astype(np.float32))
+        kc = O.bf16_round((r.standard_normal((1, 3, 1000, 128)) * scale).astype(np.float32))
+        cases.append((f"gaussian x{scale}", qc, kc))
+    # small integers: dots are exact in fp32, many land on bf16 rounding midpoints (ties to even)
+    qi = r.integers(-4, 5, size=(1, 2, 37, 128)).astype(np.float32)
+    ki = r.integers(-4, 5, size=(1, 2, 301, 128)).astype(np.float32)
+    cases.append(("small integers", qi, ki))
+    # subnormal bf16 entries next to large ones; overflowing products; zero rows
+    qs = O.bf16_round((r.standard_normal((1, 1, 40, 128))).astype(np.float32))
+    ks = O.bf16_round((r.standard_normal((1, 1, 70, 128))).astype(np.float32))
+    qs[0, 0, :5, :3] = np.float32(3e-39)
+    ks[0, 0, 7, 10:20] = np.float32(-1.5e-39)
+    qs[0, 0, 6, 0] = np.float32(1e30)
+    ks[0, 0, 8, 0] = np.float32(2e25)
+    qs[0, 0, 9] = 0.0
+    ks[0, 0, 11] = 0.0
+    cases.append(("subnormal / large / zero", O.bf16_round(qs), O.bf16_round(ks)))
+    return cases
+
+
+@pytest.mark.parametrize("case", range(5))
+def test_centroid_scores_bit_exact(gpu, case):
+    """bf16(bf16(Qc.Kc^T) * f32(1/sqrt(D))) from the certified MFMA pass (with its exact fp64 fallback) equals the
+    oracle's exact-dot scores bit for bit, on Gaussian centroids, integer dots on bf16 midpoints, bf16
+    subnormals, large values and zero rows."""
+    from svoo_amd.co_clustering import centroid_scores
+    from svoo_amd.ear import centroid_logits
+
+    name, qc, kc = _score_cases()[case]
+    say("centroid scores", name, qc.shape, kc.shape)
+    got = centroid_scores(bf16(qc, gpu), bf16(kc, gpu))
+    want = O.centroid_scores(qc, kc)
+    np.testing.assert_array_equal(O.bf16_bits(f32(got)), O.bf16_bits(want))
+    assert torch.equal(centroid_logits(bf16(qc, gpu), bf16(kc, gpu)), got)  # EAR's logits are the same values
+
+
 def _attn_check(out, ref):
     o = f32(out).astype(np.float64).reshape(-1)
     r = np.asarray(ref, np.float64).reshape(-1)

@@ -37,7 +37,11 @@ def test_library_reports_errors_without_launching():
     assert L.svoo_version() == 100
     rc = L.svoo_vbsa_fwd(None, None, None, None, None, None, None, 1, 1, 128, 1, 1, None, 0, None, None)
     assert rc == -1 and "null pointer" in _lib.last_error()
-    rc = L.svoo_block_mask(1, 1, 1, 1, 1, 1, 1, 1, 1, 64, 0.5, 0, 1, None, None)
+    rc = L.svoo_block_mask(1, 1, 1, 1, 1, 1, 1, 1, 1, 64, 0.5, 0, 1, None, 1, None)
+    assert rc == -2 and "D=64" in _lib.last_error()
+    rc = L.svoo_block_mask(1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 0.5, 0, 1, None, None, None)
+    assert rc == -1 and "null pointer" in _lib.last_error()  # the scores buffer is required
+    rc = L.svoo_centroid_scores(1, 1, 1, 1, 1, 64, 1, None)
     assert rc == -2 and "D=64" in _lib.last_error()
     assert L.svoo_co_cluster_workspace_size(40, 75600, 100, 1000, 128) > 0
 
