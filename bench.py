@@ -765,7 +765,7 @@ def cpu_baseline_dit(model, lat, txt, rho, top_p, dmin, dmax, nheads, t_step_ms,
     import numpy as np
     import torch
 
-    from oracle import svoo_oracle as O
+    from oracle import torch_ref as T
     from svoo_amd import dit
 
     cfg = model.config
@@ -792,16 +792,18 @@ def cpu_baseline_dit(model, lat, txt, rho, top_p, dmin, dmax, nheads, t_step_ms,
             v = attn.to_v(hidden_states).unflatten(2, (attn.heads, -1))
             q, k = dit.apply_rope(q, *rotary_emb), dit.apply_rope(k, *rotary_emb)
             sel = list(range(nheads))
-            qn, kn, vn = (t.transpose(1, 2)[:, sel].numpy() for t in (q, k, v))
-            n = qn.shape[2]
+            qt, kt, vt = (t.transpose(1, 2)[:, sel].contiguous() for t in (q, k, v))
+            n = qt.shape[2]
             r = np.random.default_rng(0)
+            qi = torch.from_numpy(r.integers(0, n, (nheads, 256)))
+            ki = torch.from_numpy(r.integers(0, n, (nheads, 1024)))
+            qc0 = torch.gather(qt[0], 1, qi[..., None].expand(-1, -1, d))
+            kc0 = torch.gather(kt[0], 1, ki[..., None].expand(-1, -1, d))
             t0 = time.perf_counter()
-            o = O.svoo_attention_call(qn, kn, vn, 256, 1024, 2, top_p, ratios[:nheads],
-                                      init_q_idx=r.integers(0, n, (nheads, 256)),
-                                      init_k_idx=r.integers(0, n, (nheads, 1024)), attn_dtype=np.float32)
+            o = T.svoo_attention_call(qt, kt, vt, 256, 1024, 2, top_p, ratios[:nheads], qc0, kc0)
             timing["attn"] = time.perf_counter() - t0
             out = torch.zeros(1, n, heads * d)
-            out[..., : nheads * d] = torch.from_numpy(np.asarray(o, np.float32)).reshape(1, n, nheads * d)
+            out[..., : nheads * d] = o.reshape(1, n, nheads * d)
             return attn.to_out[0](out)
 
     block.attn1.set_processor(OracleProc())
@@ -812,15 +814,15 @@ def cpu_baseline_dit(model, lat, txt, rho, top_p, dmin, dmax, nheads, t_step_ms,
     t_rest = t_block - timing["attn"]
     t_block_scaled = t_rest + timing["attn"] * heads / nheads
     step_s = t_block_scaled * cfg.num_layers
-    log(f"CPU: block {t_block:.1f}s (oracle attention {timing['attn']:.1f}s for {nheads} head(s)) -> "
+    log(f"CPU: block {t_block:.1f}s (SVOO attention {timing['attn']:.1f}s for {nheads} head(s)) -> "
         f"{step_s:.0f}s per step")
     return {
         "value": round(step_s * 1e3, 1),
         "unit": "ms per denoising step",
-        "cores": cpu_threads(),
+        "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"block 0 on the host in float32 (torch for projections, norms, cross-attention and FFN; the numpy "
-                  f"oracle for the SVOO self-attention on {nheads} of {heads} heads): {t_block:.1f} s, attention "
+        "sample": f"block 0 on the host in float32 (torch for projections, norms, cross-attention and FFN; the torch "
+                  f"restatement of the reference's SVOO self-attention on {nheads} of {heads} heads): {t_block:.1f} s, attention "
                   f"scaled x{heads / nheads:g}, block scaled x{cfg.num_layers} = {step_s:.0f} s per step = "
                   f"{step_s * 1e3 / t_step_ms:.0f}x the GPU step",
         "step_s_scaled": round(step_s, 1),
@@ -831,34 +833,40 @@ CPU_BUDGET_S = 30.0  # the CPU sample repeats (up to 3 runs, median) while its t
 
 
 def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms, hunyuan=False, ear=False):
-    """The numpy oracle on a fixed subset of ``nheads`` heads of the same inputs (heads spread evenly: 0 and H/2
-    for two), timed up to 3 times within CPU_BUDGET_S (median); latency scaled linearly to all heads."""
+    """The reference's call on the host on a fixed subset of ``nheads`` heads of the same inputs (heads spread
+    evenly: 0 and H/2 for two), timed up to 3 times within CPU_BUDGET_S (median); latency scaled linearly to all
+    heads.  SAP (Wan and HunyuanVideo): the float32 torch restatement of the reference's operations
+    (``oracle/torch_ref.py``, torch's multi-threaded CPU kernels); EAR: the numpy oracle."""
     import numpy as np
+    import torch
 
     from oracle import svoo_oracle as O
+    from oracle import torch_ref as T
 
     h, n, d = cfg.heads, cfg.tokens, cfg.head_dim
     nheads = max(1, min(nheads, h))
     sel = sorted({(i * h) // nheads for i in range(nheads)})
     nheads = len(sel)
-    f = lambda t: t[:, sel].float().cpu().numpy()  # noqa: E731
-    qn, kn, vn = f(q), f(k), f(v)
-    qi = q_init.view(h, -1, d)[sel].float().cpu().numpy()
-    ki = k_init.view(h, -1, d)[sel].float().cpu().numpy()
+    f = lambda t: t[:, sel].float().cpu().contiguous()  # noqa: E731
+    qt, kt, vt = f(q), f(k), f(v)
+    qit = q_init.view(h, -1, d)[sel].float().cpu().contiguous()
+    kit = k_init.view(h, -1, d)[sel].float().cpu().contiguous()
+    qn, kn, vn, qi, ki = (x.numpy() for x in (qt, kt, vt, qit, kit))
     rs = [ratios[i] for i in sel]
+    what = "the numpy oracle" if ear else "the float32 torch restatement of the reference's operations"
 
     def one_run():
         t0 = time.perf_counter()
-        if hunyuan:
-            O.hunyuan_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p,
-                                     rs, cfg.text_tokens, cfg.text_tokens, init_q_centroids=qi, init_k_centroids=ki,
-                                     attn_dtype=np.float32)
-        elif ear:
-            O.ear_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
-                                 1.0, init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
-        else:
-            O.svoo_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p, rs,
-                                  init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
+        with torch.no_grad():
+            if hunyuan:
+                T.hunyuan_attention_call(qt, kt, vt, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters,
+                                         top_p, rs, cfg.text_tokens, cfg.text_tokens, qit, kit)
+            elif ear:
+                O.ear_attention_call(qn, kn, vn, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p,
+                                     rs, 1.0, init_q_centroids=qi, init_k_centroids=ki, attn_dtype=np.float32)
+            else:
+                T.svoo_attention_call(qt, kt, vt, cfg.num_q_centroids, cfg.num_k_centroids, cfg.kmeans_iters, top_p,
+                                      rs, qit, kit)
         return time.perf_counter() - t0
 
     runs = [one_run()]
@@ -867,15 +875,15 @@ def cpu_baseline(cfg, q, k, v, q_init, k_init, top_p, ratios, nheads, t_call_ms,
     t = float(np.median(runs))
     per_head = t / nheads
     call_s = per_head * h
-    log(f"CPU oracle: {[round(x, 2) for x in runs]} s for heads {sel} -> {call_s:.1f}s per {h}-head call")
+    log(f"CPU ({what}): {[round(x, 2) for x in runs]} s for heads {sel} -> {call_s:.1f}s per {h}-head call")
     return {
         "value": round(4.0 * nheads * float(n) ** 2 * d / t / 1e12, 5),
         "unit": "TFLOP/s (dense-equivalent)",
-        "cores": cpu_threads(),
+        "cores": torch.get_num_threads() if not ear else cpu_threads(),
         "kind": "port",
         "sample": f"heads {sel} of {h} of the same inputs, full call (k-means {cfg.kmeans_iters} warm-started "
                   f"iterations, {'EAR scoring and selection' if ear else 'mask'}, permutes, fp32 "
-                  f"{'compensated ' if ear else ''}block-sparse attention) in the numpy oracle: median of "
+                  f"{'compensated ' if ear else ''}block-sparse attention) in {what}: median of "
                   f"{len(runs)} run(s) {t:.2f} s; scaled x{h / nheads:g} to {call_s:.1f} s per call = "
                   f"{call_s * 1e3 / t_call_ms:.0f}x the GPU latency",
         "call_s_scaled": round(call_s, 3),
