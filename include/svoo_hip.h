@@ -88,6 +88,15 @@ int svoo_centroid_update(const uint16_t* x, const int32_t* sorted_idx, const int
 int svoo_l2norm_rows(const void* x, int x_is_bf16, float* y, long long rows, int cols, float eps, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Element-type conversion of n contiguous values: types 0 bf16, 1 fp16, 2 fp32; to bf16 / fp16 by rounding to
+ * nearest even (through fp32).  The operators take fp16 and fp32 tensors by rounding them to bf16, the type
+ * every kernel here computes in, and return results in the caller's type; the reference's Triton kernels load
+ * any float input as fp32 (svoo/co_clustering.py:2121, :2197) and FlashInfer takes fp16 or bf16
+ * (svoo/utils/flashinfer_sparse.py:117-124).
+ * ------------------------------------------------------------------------------------------- */
+int svoo_convert(const void* src, int src_type, void* dst, int dst_type, long long n, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Co-clustering (profile-space k-means).
  *   svoo_cocluster_prep: P = l2norm(bf16(A B^T)) ([BH][J][KP], optional output), E = P B split into
  *     E_hi = bf16(E), E_lo = bf16(E - E_hi), both [BH][jpad][D]; rows J..jpad-1 repeat row J-1.

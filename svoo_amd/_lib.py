@@ -29,6 +29,7 @@ _SIGS = {
     "svoo_centroid_update_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "svoo_centroid_update": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
     "svoo_l2norm_rows": (c_int, [P, c_int, P, c_longlong, c_int, c_float, P]),
+    "svoo_convert": (c_int, [P, c_int, P, c_int, c_longlong, P]),
     "svoo_cocluster_prep": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "svoo_cocluster_assign": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "svoo_co_cluster_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
@@ -105,6 +106,32 @@ def stream_of(device: torch.device) -> int:
 def require_gpu_tensor(t: torch.Tensor, name: str) -> None:
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise AssertionError(f"{name} must be a GPU (HIP) tensor")
+
+
+_ELEM_TYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def convert(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """``x`` in ``dtype`` through the HIP conversion kernel (bf16 / fp16 / fp32; rounding to nearest even)."""
+    if x.dtype == dtype:
+        return x
+    if x.dtype not in _ELEM_TYPES or dtype not in _ELEM_TYPES:
+        raise TypeError(f"the MI355X path takes bfloat16, float16 or float32 tensors, got {x.dtype} -> {dtype}")
+    require_gpu_tensor(x, "x")
+    xx = x.contiguous()
+    out = torch.empty(xx.shape, dtype=dtype, device=xx.device)
+    call("svoo_convert", xx.data_ptr(), _ELEM_TYPES[xx.dtype], out.data_ptr(), _ELEM_TYPES[dtype], xx.numel(),
+         stream_of(xx.device))
+    return out
+
+
+def as_bf16(x: torch.Tensor, name: str) -> torch.Tensor:
+    """The bf16 operand of a kernel: bf16 tensors as they are, fp16 / fp32 rounded to bf16 (to nearest even)."""
+    if not isinstance(x, torch.Tensor) or x.dtype not in _ELEM_TYPES:
+        raise TypeError(f"{name}: the MI355X path takes bfloat16, float16 or float32 tensors, got "
+                        f"{getattr(x, 'dtype', type(x).__name__)}")
+    require_gpu_tensor(x, name)
+    return convert(x, torch.bfloat16)
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:

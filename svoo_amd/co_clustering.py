@@ -41,12 +41,11 @@ def _pad(v: int, m: int = _ASSIGN_CHUNK) -> int:
 
 
 def _bf16_3d(x: torch.Tensor, name: str) -> torch.Tensor:
-    _lib.require_gpu_tensor(x, name)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"{name}: the MI355X path computes in bfloat16, got {x.dtype}")
-    if x.dim() != 3 or x.shape[-1] != 128:
+    """``x [BH, N, 128]`` as the kernels' bf16 operand (fp16 / fp32 rounded to bf16, to nearest even)."""
+    xx = _lib.as_bf16(x, name)
+    if xx.dim() != 3 or xx.shape[-1] != 128:
         raise ValueError(f"{name}: expected [BH, N, 128], got {tuple(x.shape)}")
-    return x.contiguous()
+    return xx.contiguous()
 
 
 # ------------------------------------------------------------------------------------------------
@@ -78,9 +77,10 @@ def co_cluster_tokens_full(
 ) -> dict:
     """:func:`co_cluster_tokens` returning every device output in a dict.
 
-    Keys: ``qlabels, klabels`` (int32), ``qcentroids, kcentroids`` (bf16), ``qsizes, ksizes``,
+    Keys: ``qlabels, klabels`` (int32), ``qcentroids, kcentroids`` (in the tokens' dtype), ``qsizes, ksizes``,
     ``q_sorted_idx, k_sorted_idx`` and ``q_offsets, k_offsets`` (int32; the stable cluster sort of
-    the final labels, ready for the permutes).
+    the final labels, ready for the permutes).  fp16 / fp32 tokens and centroids are rounded to bf16, the type
+    the kernels compute in; the centroids come back in the tokens' dtype (bf16 values).
     """
     q = _bf16_3d(q_flat, "q_flat")
     k = _bf16_3d(k_flat, "k_flat")
@@ -93,7 +93,7 @@ def co_cluster_tokens_full(
 
     def _init(x, idx, cents, nc):
         if cents is not None:
-            c = cents.to(device=dev, dtype=torch.bfloat16).reshape(bh, nc, d)
+            c = _lib.as_bf16(cents.to(device=dev), "init centroids").reshape(bh, nc, d)
             return c.clone()
         if idx is None:
             # svoo/co_clustering.py:2417-2421: uniform random token indices (with replacement).
@@ -117,8 +117,8 @@ def co_cluster_tokens_full(
         out["ksizes"].data_ptr(), out["q_sorted_idx"].data_ptr(), out["k_sorted_idx"].data_ptr(),
         out["q_offsets"].data_ptr(), out["k_offsets"].data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(dev),
     )
-    out["qcentroids"] = qc
-    out["kcentroids"] = kc
+    out["qcentroids"] = _lib.convert(qc, q_flat.dtype)
+    out["kcentroids"] = _lib.convert(kc, q_flat.dtype)
     return out
 
 
@@ -191,7 +191,7 @@ def centroid_update(x: torch.Tensor, labels: torch.Tensor, old_centroids: torch.
     """Cluster means of ``x`` by ``labels``; empty clusters keep ``old_centroids``.
 
     Mirrors ``triton_centroid_update_sorted_euclid`` (``svoo/co_clustering.py:253-303``): returns
-    ``(centroids bf16 [BH, K, 128], counts int32 [BH, K])``.
+    ``(centroids [BH, K, 128] in x's dtype, counts int32 [BH, K])``; fp16 / fp32 inputs are rounded to bf16.
     """
     from .permute import cluster_sort  # local import keeps module load order simple
 
@@ -206,7 +206,7 @@ def centroid_update(x: torch.Tensor, labels: torch.Tensor, old_centroids: torch.
     ws = _lib.workspace(L.svoo_centroid_update_workspace_size(bh, k, d), xx.device)
     _lib.call("svoo_centroid_update", xx.data_ptr(), sorted_idx.data_ptr(), sorted_lab.data_ptr(), sizes.data_ptr(),
               old.data_ptr(), new.data_ptr(), bh, n, k, d, ws.data_ptr(), ws.numel(), _lib.stream_of(xx.device))
-    return new, sizes
+    return _lib.convert(new, x.dtype), sizes
 
 
 def triton_l2norm_forward(x: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
@@ -215,7 +215,7 @@ def triton_l2norm_forward(x: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
     assert x.dim() in (2, 3), "Input tensors must be batched (3D) or not batched (2D)"
     xx = x.contiguous()
     if xx.dtype not in (torch.bfloat16, torch.float32):
-        xx = xx.float()
+        xx = _lib.convert(xx, torch.float32)
     y = torch.empty(xx.shape, dtype=torch.float32, device=xx.device)
     rows = xx.numel() // xx.shape[-1]
     _lib.call("svoo_l2norm_rows", xx.data_ptr(), int(xx.dtype == torch.bfloat16), y.data_ptr(), rows, xx.shape[-1],
@@ -227,11 +227,9 @@ def triton_l2norm_forward(x: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
 # Block mask
 # ------------------------------------------------------------------------------------------------
 def weighted_softmax(scores: torch.Tensor, weights: torch.Tensor) -> torch.Tensor:
-    """Softmax after weighting each key cluster by its size (``svoo/co_clustering.py:544-553``), bf16 in/out."""
-    _lib.require_gpu_tensor(scores, "scores")
-    if scores.dtype != torch.bfloat16:
-        raise TypeError("weighted_softmax: the MI355X path takes bfloat16 scores")
-    s = scores.contiguous()
+    """Softmax after weighting each key cluster by its size (``svoo/co_clustering.py:544-553``).  Computed on bf16
+    scores (fp16 / fp32 scores are rounded to bf16) with a bf16 result, returned in the scores' dtype."""
+    s = _lib.as_bf16(scores, "scores").contiguous()
     cols = s.shape[-1]
     rows = s.numel() // cols
     w = weights.to(device=s.device, dtype=torch.float32)
@@ -239,7 +237,7 @@ def weighted_softmax(scores: torch.Tensor, weights: torch.Tensor) -> torch.Tenso
     out = torch.empty_like(s)
     _lib.call("svoo_weighted_softmax", s.data_ptr(), w.data_ptr(), cols, out.data_ptr(), rows, cols,
               _lib.stream_of(s.device))
-    return out
+    return _lib.convert(out, scores.dtype)
 
 
 def _ratio_values(v, h: int):
@@ -317,8 +315,8 @@ def block_mask_lengths(query_centroids, key_centroids, q_cluster_sizes, k_cluste
         _lib.call("svoo_block_mask", None, None, None, None, None, b, h, qn, kn, d, 0.0, 1, dmap.data_ptr(),
                   lengths.data_ptr(), None, _lib.stream_of(dev))
         return dmap, lengths
-    if qc.dtype != torch.bfloat16 or kc.dtype != torch.bfloat16:
-        raise TypeError("identify_dynamic_map: the MI355X path takes bfloat16 centroids")
+    qc = _lib.as_bf16(qc, "query_centroids")
+    kc = _lib.as_bf16(kc, "key_centroids")
     preserve, cap = mask_row_params(h, kn, min_kc_ratio, max_kc_ratio)
     pc = torch.tensor(preserve + cap, dtype=torch.int32).to(dev, non_blocking=True)
     ks = k_cluster_sizes.to(device=dev, dtype=torch.int32).reshape(b * h, kn).contiguous()
@@ -333,10 +331,8 @@ def centroid_scores(query_centroids, key_centroids) -> torch.Tensor:
     """Scaled centroid attention scores ``matmul(Qc, Kc^T) / D**0.5`` of the block mask on bf16 centroids
     (``svoo/co_clustering.py:578``): the exact dot rounded to bf16, times ``float32(1 / sqrt(D))``, rounded to
     bf16.  ``[B, H, Qc, D]`` x ``[B, H, Kc, D]`` -> ``[B, H, Qc, Kc]`` bf16."""
-    qc, kc = query_centroids, key_centroids
-    _lib.require_gpu_tensor(qc, "query_centroids")
-    if qc.dtype != torch.bfloat16 or kc.dtype != torch.bfloat16:
-        raise TypeError("centroid_scores: the MI355X path takes bfloat16 centroids")
+    qc = _lib.as_bf16(query_centroids, "query_centroids")
+    kc = _lib.as_bf16(key_centroids, "key_centroids")
     b, h, qn, d = qc.shape
     kn = kc.shape[2]
     out = torch.empty(b, h, qn, kn, dtype=torch.bfloat16, device=qc.device)
@@ -383,8 +379,8 @@ def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate
     """
     assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
     assert q.dtype == k.dtype == v.dtype, "Input dtypes must match"
-    if q.dtype != torch.bfloat16:
-        raise TypeError("dynamic_block_sparse_fwd: the MI355X path computes in bfloat16")
+    in_dtype = q.dtype
+    q, k, v = (_lib.as_bf16(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     b, h, s, d = q.shape
     assert k.shape == q.shape and v.shape == q.shape, "q, k, v must share one shape"
     qn = qc_size.shape[-1]
@@ -409,7 +405,7 @@ def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate
               _lib.stream_of(dev))
     if validate and int(status.item()) != 0:
         raise AssertionError("cluster sizes of every head must sum to S (qc_size / kc_size)")
-    return out.reshape(b, h, s, d)
+    return _lib.convert(out.reshape(b, h, s, d), in_dtype)
 
 
 def dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, qc_size, kc_size, q_sorted_idx, k_sorted_idx,
@@ -422,8 +418,9 @@ def dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, qc_size, kc_s
     ``transpose(1, 2).flatten(2, 3)`` (``svoo/models/wan/attention.py:1037-1042, 1196-1215``).
     """
     assert query.is_cuda and key.is_cuda and value.is_cuda, "Inputs must be CUDA tensors"
-    if query.dtype != torch.bfloat16 or key.dtype != query.dtype or value.dtype != query.dtype:
-        raise TypeError("dynamic_block_sparse_fwd_fused: the MI355X path computes in bfloat16")
+    assert query.dtype == key.dtype == value.dtype, "Input dtypes must match"
+    in_dtype = query.dtype
+    query, key, value = (_lib.as_bf16(t, n) for t, n in ((query, "query"), (key, "key"), (value, "value")))
     b, h, s, d = query.shape
     assert key.shape == query.shape and value.shape == query.shape, "q, k, v must share one shape"
     qn = qc_size.shape[-1]
@@ -448,7 +445,7 @@ def dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, qc_size, kc_s
               ws.numel(), _lib.ptr(status), _lib.stream_of(dev))
     if validate and int(status.item()) != 0:
         raise AssertionError("cluster sizes of every head must sum to S (qc_size / kc_size)")
-    return out
+    return _lib.convert(out, in_dtype)
 
 
 def dynamic_block_sparse_fwd_flashinfer(q, k, v, block_mask_map, block_row_sz, block_col_sz, is_cpu: bool = True):

@@ -39,12 +39,11 @@ EAR_EPS = 1e-8  # identify_dynamic_map_estimated's eps (svoo/co_clustering.py:17
 
 
 def _bf16_4d(x: torch.Tensor, name: str) -> torch.Tensor:
-    _lib.require_gpu_tensor(x, name)
-    if x.dtype != torch.bfloat16:
-        raise TypeError(f"{name}: the MI355X path computes in bfloat16, got {x.dtype}")
-    if x.dim() != 4 or x.shape[-1] != 128:
+    """``x [B, H, N, 128]`` as the kernels' bf16 operand (fp16 / fp32 rounded to bf16, to nearest even)."""
+    xx = _lib.as_bf16(x, name)
+    if xx.dim() != 4 or xx.shape[-1] != 128:
         raise ValueError(f"{name}: expected [B, H, N, 128], got {tuple(x.shape)}")
-    return x.contiguous()
+    return xx.contiguous()
 
 
 def _sizes(x: torch.Tensor, dev, bh: int, n: int) -> torch.Tensor:
@@ -101,13 +100,13 @@ def _value_stats(v_perm: torch.Tensor, ks: torch.Tensor, koff: torch.Tensor, vc:
 
 def value_centroids_from_permuted(v_perm: torch.Tensor, k_cluster_sizes: torch.Tensor) -> torch.Tensor:
     """Value centroids ``[B, H, Kc, D]`` of cluster-contiguous values ``v_perm [B, H, S, D]``:
-    ``bf16(bf16(member sum) / bf16(max(|K_j|, 1)))``, zero for an empty cluster."""
+    ``bf16(bf16(member sum) / bf16(max(|K_j|, 1)))``, zero for an empty cluster; in v_perm's dtype."""
     vp = _bf16_4d(v_perm, "v_perm")
     b, h, s, d = vp.shape
     kn = k_cluster_sizes.shape[-1]
     ks = _sizes(k_cluster_sizes, vp.device, b * h, kn)
     vc, _, _ = _value_stats(vp.reshape(b * h, s, d), ks, _offsets(ks), None)
-    return vc.reshape(b, h, kn, d)
+    return _lib.convert(vc.reshape(b, h, kn, d), v_perm.dtype)
 
 
 def compute_value_centroids(tokens: torch.Tensor, labels: torch.Tensor, cluster_sizes: torch.Tensor,
@@ -137,7 +136,7 @@ def centroid_logits(query_centroids: torch.Tensor, key_centroids: torch.Tensor) 
     c = torch.empty(b, h, qn, kn, dtype=torch.bfloat16, device=qc.device)
     _lib.call("svoo_ear_centroid_logits", qc.data_ptr(), kc.data_ptr(), b * h, qn, kn, d, c.data_ptr(),
               _lib.stream_of(qc.device))
-    return c
+    return _lib.convert(c, query_centroids.dtype)
 
 
 def _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma: float, eps: float) -> torch.Tensor:
@@ -168,7 +167,7 @@ def error_estimation_triton(query_centroids, key_centroids, value_centroids, per
     koff = _offsets(ks)
     vc = _bf16_4d(value_centroids, "value_centroids")
     _, vc_sq, stats = _value_stats(vp.reshape(b * h, s, d), ks, koff, vc)
-    c = c_logits.to(torch.bfloat16).contiguous()
+    c = _lib.as_bf16(c_logits, "c_logits").contiguous()
     return _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma, eps)
 
 
@@ -213,7 +212,7 @@ def identify_dynamic_map_estimated(q_perm, k_perm, v_perm, qc_sz, kc_sz, qcentro
 def ear_map_and_value_centroids(q_perm, k_perm, v_perm, qc_sz, kc_sz, qcentroids, kcentroids, top_p=0.9,
                                 gamma=1.0, min_kc_ratio=0.0, return_parts: bool = False):
     """Value centroids and EAR map in one pass over ``v_perm`` (the processor's path): returns
-    ``(v_centroids [B, H, Kc, D], map)``, plus ``{"c", "eff"}`` with ``return_parts``."""
+    ``(v_centroids [B, H, Kc, D] in v_perm's dtype, map)``, plus ``{"c", "eff"}`` with ``return_parts``."""
     qc = _bf16_4d(qcentroids, "qcentroids")
     b, h, qn, d = qc.shape
     kn = kcentroids.shape[2]
@@ -228,7 +227,7 @@ def ear_map_and_value_centroids(q_perm, k_perm, v_perm, qc_sz, kc_sz, qcentroids
     c = centroid_logits(qc, kcentroids)
     eff = _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma, EAR_EPS)
     dmap = _select(c, eff, qs, ks, b, h, qn, kn, top_p, min_kc_ratio)
-    vc = vc.reshape(b, h, kn, d)
+    vc = _lib.convert(vc.reshape(b, h, kn, d), v_perm.dtype)
     if return_parts:
         return vc, dmap, {"c": c, "eff": eff}
     return vc, dmap
@@ -244,8 +243,9 @@ def dynamic_block_sparse_prune_fwd(q, k, v, k_centroids, v_centroids, block_mask
     log(|K_j| + 1e-6)``.  With ``validate`` the sizes of every head must sum to ``S``; host-side sizes
     are checked before the launch, and without ``validate`` inconsistent device sizes give NaN rows."""
     assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
-    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise TypeError("dynamic_block_sparse_prune_fwd: the MI355X path computes in bfloat16")
+    assert q.dtype == k.dtype == v.dtype, "Input dtypes must match"
+    in_dtype = q.dtype
+    q, k, v = (_lib.as_bf16(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     b, h, s, d = q.shape
     qn = block_row_sz.shape[-1]
     kn = block_col_sz.shape[-1]
@@ -271,7 +271,7 @@ def dynamic_block_sparse_prune_fwd(q, k, v, k_centroids, v_centroids, block_mask
               _lib.ptr(status), _lib.stream_of(dev))
     if validate and int(status.item()) != 0:
         raise AssertionError("cluster sizes of every head must sum to S (block_row_sz / block_col_sz)")
-    return out.reshape(b, h, s, d)
+    return _lib.convert(out.reshape(b, h, s, d), in_dtype)
 
 
 def dynamic_block_sparse_prune_fwd_flashinfer(q, k, v, k_centroids, v_centroids, block_mask_map, block_row_sz,

@@ -3,8 +3,9 @@ call, H=2, N=4680, 32/64 clusters, density 0.25) end to end against the oracle, 
 Wan2.1-1.3B DiT with SVOO in all 30 blocks, three steps with carried centroids), and the incremental centroid
 update against a full recount on an input whose magnitudes span 40 binades.
 
-C1 is specified in fp32; the MI355X path computes in bf16 only, so the inputs are rounded to bf16 and the oracle
-runs on the rounded values (its attention in float64)."""
+C1 is specified in fp32; the MI355X path computes in bf16, so here the inputs are rounded to bf16 and the oracle runs
+on the rounded values (its attention in float64).  The fp32 call itself equals this call bit for bit
+(``test_gpu_dtypes.py::test_c1_processor_call_in_fp32``)."""
 
 import numpy as np
 import pytest

@@ -44,6 +44,27 @@ def test_library_reports_errors_without_launching():
     rc = L.svoo_centroid_scores(1, 1, 1, 1, 1, 64, 1, None)
     assert rc == -2 and "D=64" in _lib.last_error()
     assert L.svoo_co_cluster_workspace_size(40, 75600, 100, 1000, 128) > 0
+    rc = L.svoo_convert(1, 0, 1, 3, 8, None)
+    assert rc == -1 and "element types" in _lib.last_error()
+    rc = L.svoo_convert(None, 0, 1, 2, 8, None)
+    assert rc == -1 and "null pointer" in _lib.last_error()
+    assert L.svoo_convert(1, 2, 1, 0, 0, None) == 0  # nothing to convert: no launch
+
+
+def test_operators_reject_non_float_inputs_before_any_call():
+    """Operands are bf16, fp16 or fp32 (fp16 / fp32 are rounded to bf16 on the GPU); anything else is refused
+    on the host, before a GPU is touched."""
+    from svoo_amd import _lib
+    from svoo_amd.co_clustering import co_cluster_tokens_full, dynamic_block_sparse_fwd
+
+    with pytest.raises(TypeError, match="bfloat16, float16 or float32"):
+        _lib.as_bf16(torch.zeros(2, 3, 128, dtype=torch.int32), "x")
+    with pytest.raises(TypeError, match="float64"):
+        co_cluster_tokens_full(torch.zeros(1, 64, 128, dtype=torch.float64), torch.zeros(1, 64, 128), 4, 4, 1)
+    with pytest.raises(AssertionError, match="GPU"):
+        _lib.as_bf16(torch.zeros(2, 3, 128), "x")  # a float tensor on the CPU
+    with pytest.raises(AssertionError, match="CUDA"):
+        dynamic_block_sparse_fwd(*(torch.zeros(1, 1, 8, 128),) * 3, None, None, None)
 
 
 def test_noalloc_attention_rejects_plans_above_its_scratch():
