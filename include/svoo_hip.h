@@ -9,8 +9,12 @@
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Every entry point only
  *     enqueues work on that stream and never synchronises the host.
  *   - Return value: SVOO_OK (0) or a negative SVOO_ERR_* code; svoo_last_error() describes the failure.
- *   - Shapes use the reference's names: BH = batch*heads, N/S = tokens, D = head dim (128 only),
- *     QC/KC = query/key cluster counts.
+ *   - Shapes use the reference's names: BH = batch*heads, N/S = tokens, D = head dim, QC/KC = query/key
+ *     cluster counts.
+ *   - Head dim: every row of Q, K, V and of the centroids holds 128 elements (256 bytes).  D (1..128) is the
+ *     head dim; for D < 128 elements D..127 of every row must be zero (the Python operators pad).  D sets the
+ *     score and softmax scale 1/sqrt(D); on zero-padded rows every dot, centroid and label equals that of the
+ *     D-element rows.  Outputs are rows of 128 with zeros past D.
  *
  * Reference paths below are relative to the root of the reference repository (Mutual-Luo/SVOO).
  */
@@ -95,6 +99,10 @@ int svoo_l2norm_rows(const void* x, int x_is_bf16, float* y, long long rows, int
  * (svoo/utils/flashinfer_sparse.py:117-124).
  * ------------------------------------------------------------------------------------------- */
 int svoo_convert(const void* src, int src_type, void* dst, int dst_type, long long n, void* stream);
+/* rows[r] of src_cols elements -> rows of dst_cols: the first min(src_cols, dst_cols) converted, the rest zero
+ * (the padding of a head dim below 128 and its removal). */
+int svoo_convert_rows(const void* src, int src_type, int src_cols, void* dst, int dst_type, int dst_cols,
+                      long long rows, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Co-clustering (profile-space k-means).

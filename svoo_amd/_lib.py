@@ -30,6 +30,7 @@ _SIGS = {
     "svoo_centroid_update": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
     "svoo_l2norm_rows": (c_int, [P, c_int, P, c_longlong, c_int, c_float, P]),
     "svoo_convert": (c_int, [P, c_int, P, c_int, c_longlong, P]),
+    "svoo_convert_rows": (c_int, [P, c_int, c_int, P, c_int, c_int, c_longlong, P]),
     "svoo_cocluster_prep": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "svoo_cocluster_assign": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "svoo_co_cluster_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
@@ -132,6 +133,39 @@ def as_bf16(x: torch.Tensor, name: str) -> torch.Tensor:
                         f"{getattr(x, 'dtype', type(x).__name__)}")
     require_gpu_tensor(x, name)
     return convert(x, torch.bfloat16)
+
+
+ROW = 128  # elements per row of every kernel operand; head dims below it are zero-padded
+
+
+def as_rows128(x: torch.Tensor, name: str) -> torch.Tensor:
+    """``x [..., D]`` (D <= 128; bf16 / fp16 / fp32) as the kernels' bf16 operand ``[..., 128]``: fp16 / fp32 rounded
+    to bf16 (to nearest even), columns past D zero."""
+    if not isinstance(x, torch.Tensor) or x.dtype not in _ELEM_TYPES:
+        raise TypeError(f"{name}: the MI355X path takes bfloat16, float16 or float32 tensors, got "
+                        f"{getattr(x, 'dtype', type(x).__name__)}")
+    d = x.shape[-1] if x.dim() else 0
+    if not 1 <= d <= ROW:
+        raise ValueError(f"{name}: head dim {d} (the MI355X path takes 1..{ROW})")
+    if d == ROW:
+        return as_bf16(x, name)
+    require_gpu_tensor(x, name)
+    xx = x.contiguous()
+    out = torch.empty(*xx.shape[:-1], ROW, dtype=torch.bfloat16, device=xx.device)
+    call("svoo_convert_rows", xx.data_ptr(), _ELEM_TYPES[xx.dtype], d, out.data_ptr(), 0, ROW, xx.numel() // d,
+         stream_of(xx.device))
+    return out
+
+
+def from_rows128(y: torch.Tensor, d: int, dtype: torch.dtype) -> torch.Tensor:
+    """Rows of 128 back to the caller's head dim ``d`` (the first d columns) and dtype."""
+    if d == ROW:
+        return convert(y, dtype)
+    yy = y.contiguous()
+    out = torch.empty(*yy.shape[:-1], d, dtype=dtype, device=yy.device)
+    call("svoo_convert_rows", yy.data_ptr(), _ELEM_TYPES[yy.dtype], ROW, out.data_ptr(), _ELEM_TYPES[dtype], d,
+         yy.numel() // ROW, stream_of(yy.device))
+    return out
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:

@@ -41,11 +41,11 @@ def _pad(v: int, m: int = _ASSIGN_CHUNK) -> int:
 
 
 def _bf16_3d(x: torch.Tensor, name: str) -> torch.Tensor:
-    """``x [BH, N, 128]`` as the kernels' bf16 operand (fp16 / fp32 rounded to bf16, to nearest even)."""
-    xx = _lib.as_bf16(x, name)
-    if xx.dim() != 3 or xx.shape[-1] != 128:
-        raise ValueError(f"{name}: expected [BH, N, 128], got {tuple(x.shape)}")
-    return xx.contiguous()
+    """``x [BH, N, D]`` (D <= 128) as the kernels' bf16 operand ``[BH, N, 128]`` (fp16 / fp32 rounded to bf16, to
+    nearest even; columns past D zero, which leaves every dot, centroid and label as on the D columns)."""
+    if isinstance(x, torch.Tensor) and x.dim() != 3:
+        raise ValueError(f"{name}: expected [BH, N, D], got {tuple(x.shape)}")
+    return _lib.as_rows128(x, name).contiguous()
 
 
 # ------------------------------------------------------------------------------------------------
@@ -82,18 +82,19 @@ def co_cluster_tokens_full(
     the final labels, ready for the permutes).  fp16 / fp32 tokens and centroids are rounded to bf16, the type
     the kernels compute in; the centroids come back in the tokens' dtype (bf16 values).
     """
+    assert q_flat.shape == k_flat.shape, "q_flat and k_flat must have the same shape"
     q = _bf16_3d(q_flat, "q_flat")
     k = _bf16_3d(k_flat, "k_flat")
-    assert q.shape == k.shape, "q_flat and k_flat must have the same shape"
     if max_iters < 1:
         # svoo/co_clustering.py:2451 returns qlabels, which the loop never bound.
         raise UnboundLocalError("co_cluster_tokens needs max_iters >= 1")
     bh, n, d = q.shape
+    hd = q_flat.shape[-1]
     dev = q.device
 
     def _init(x, idx, cents, nc):
         if cents is not None:
-            c = _lib.as_bf16(cents.to(device=dev), "init centroids").reshape(bh, nc, d)
+            c = _lib.as_rows128(cents.to(device=dev).reshape(bh, nc, hd), "init centroids")
             return c.clone()
         if idx is None:
             # svoo/co_clustering.py:2417-2421: uniform random token indices (with replacement).
@@ -112,13 +113,13 @@ def co_cluster_tokens_full(
     L = _lib.lib()
     ws = _lib.workspace(L.svoo_co_cluster_workspace_size(bh, n, num_q_centroids, num_k_centroids, d), dev)
     _lib.call(
-        "svoo_co_cluster", q.data_ptr(), k.data_ptr(), bh, n, d, num_q_centroids, num_k_centroids, max_iters,
+        "svoo_co_cluster", q.data_ptr(), k.data_ptr(), bh, n, hd, num_q_centroids, num_k_centroids, max_iters,
         qc.data_ptr(), kc.data_ptr(), out["qlabels"].data_ptr(), out["klabels"].data_ptr(), out["qsizes"].data_ptr(),
         out["ksizes"].data_ptr(), out["q_sorted_idx"].data_ptr(), out["k_sorted_idx"].data_ptr(),
         out["q_offsets"].data_ptr(), out["k_offsets"].data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(dev),
     )
-    out["qcentroids"] = _lib.convert(qc, q_flat.dtype)
-    out["kcentroids"] = _lib.convert(kc, q_flat.dtype)
+    out["qcentroids"] = _lib.from_rows128(qc, hd, q_flat.dtype)
+    out["kcentroids"] = _lib.from_rows128(kc, hd, q_flat.dtype)
     return out
 
 
@@ -153,8 +154,8 @@ def co_cluster_tokens(
 def cocluster_profile(centroids: torch.Tensor, basis: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Profile centroids ``P = l2norm(bf16(A B^T))`` and the split assignment matrix ``E = P B``.
 
-    ``centroids`` is ``A [BH, J, 128]``, ``basis`` is ``B [BH, KP, 128]`` (bf16).  Returns
-    ``(P fp32 [BH, J, KP], E_hi bf16 [BH, Jpad, 128], E_lo bf16 [BH, Jpad, 128])``; follows
+    ``centroids`` is ``A [BH, J, D]``, ``basis`` is ``B [BH, KP, D]`` (D <= 128).  Returns
+    ``(P fp32 [BH, J, KP], E_hi bf16 [BH, Jpad, 128], E_lo bf16 [BH, Jpad, 128])`` (E zero past D); follows
     ``svoo/co_clustering.py:2427-2428`` (profile) and the reduction of ``:2146-2255`` (assignment).
     """
     a = _bf16_3d(centroids, "centroids")
@@ -166,7 +167,7 @@ def cocluster_profile(centroids: torch.Tensor, basis: torch.Tensor) -> Tuple[tor
     e_hi = torch.empty(bh, jpad, 128, dtype=torch.bfloat16, device=a.device)
     e_lo = torch.empty_like(e_hi)
     _lib.call("svoo_cocluster_prep", a.data_ptr(), b.data_ptr(), e_hi.data_ptr(), e_lo.data_ptr(), prof.data_ptr(),
-              bh, j, kp, 128, jpad, _lib.stream_of(a.device))
+              bh, j, kp, centroids.shape[-1], jpad, _lib.stream_of(a.device))
     return prof, e_hi, e_lo
 
 
@@ -183,7 +184,7 @@ def cocluster_assign(x: torch.Tensor, centroids: torch.Tensor, basis: torch.Tens
     j = centroids.shape[1]
     labels = torch.empty(bh, n, dtype=torch.int32, device=xx.device)
     _lib.call("svoo_cocluster_assign", xx.data_ptr(), e_hi.data_ptr(), e_lo.data_ptr(), labels.data_ptr(), bh, n, j,
-              e_hi.shape[1], 128, _lib.stream_of(xx.device))
+              e_hi.shape[1], x.shape[-1], _lib.stream_of(xx.device))
     return labels
 
 
@@ -191,7 +192,7 @@ def centroid_update(x: torch.Tensor, labels: torch.Tensor, old_centroids: torch.
     """Cluster means of ``x`` by ``labels``; empty clusters keep ``old_centroids``.
 
     Mirrors ``triton_centroid_update_sorted_euclid`` (``svoo/co_clustering.py:253-303``): returns
-    ``(centroids [BH, K, 128] in x's dtype, counts int32 [BH, K])``; fp16 / fp32 inputs are rounded to bf16.
+    ``(centroids [BH, K, D] in x's dtype, counts int32 [BH, K])``; fp16 / fp32 inputs are rounded to bf16.
     """
     from .permute import cluster_sort  # local import keeps module load order simple
 
@@ -205,8 +206,9 @@ def centroid_update(x: torch.Tensor, labels: torch.Tensor, old_centroids: torch.
     L = _lib.lib()
     ws = _lib.workspace(L.svoo_centroid_update_workspace_size(bh, k, d), xx.device)
     _lib.call("svoo_centroid_update", xx.data_ptr(), sorted_idx.data_ptr(), sorted_lab.data_ptr(), sizes.data_ptr(),
-              old.data_ptr(), new.data_ptr(), bh, n, k, d, ws.data_ptr(), ws.numel(), _lib.stream_of(xx.device))
-    return _lib.convert(new, x.dtype), sizes
+              old.data_ptr(), new.data_ptr(), bh, n, k, x.shape[-1], ws.data_ptr(), ws.numel(),
+              _lib.stream_of(xx.device))
+    return _lib.from_rows128(new, x.shape[-1], x.dtype), sizes
 
 
 def triton_l2norm_forward(x: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
@@ -315,8 +317,8 @@ def block_mask_lengths(query_centroids, key_centroids, q_cluster_sizes, k_cluste
         _lib.call("svoo_block_mask", None, None, None, None, None, b, h, qn, kn, d, 0.0, 1, dmap.data_ptr(),
                   lengths.data_ptr(), None, _lib.stream_of(dev))
         return dmap, lengths
-    qc = _lib.as_bf16(qc, "query_centroids")
-    kc = _lib.as_bf16(kc, "key_centroids")
+    qc = _lib.as_rows128(qc, "query_centroids")
+    kc = _lib.as_rows128(kc, "key_centroids")
     preserve, cap = mask_row_params(h, kn, min_kc_ratio, max_kc_ratio)
     pc = torch.tensor(preserve + cap, dtype=torch.int32).to(dev, non_blocking=True)
     ks = k_cluster_sizes.to(device=dev, dtype=torch.int32).reshape(b * h, kn).contiguous()
@@ -331,9 +333,10 @@ def centroid_scores(query_centroids, key_centroids) -> torch.Tensor:
     """Scaled centroid attention scores ``matmul(Qc, Kc^T) / D**0.5`` of the block mask on bf16 centroids
     (``svoo/co_clustering.py:578``): the exact dot rounded to bf16, times ``float32(1 / sqrt(D))``, rounded to
     bf16.  ``[B, H, Qc, D]`` x ``[B, H, Kc, D]`` -> ``[B, H, Qc, Kc]`` bf16."""
-    qc = _lib.as_bf16(query_centroids, "query_centroids")
-    kc = _lib.as_bf16(key_centroids, "key_centroids")
-    b, h, qn, d = qc.shape
+    qc = _lib.as_rows128(query_centroids, "query_centroids")
+    kc = _lib.as_rows128(key_centroids, "key_centroids")
+    b, h, qn, _ = qc.shape
+    d = query_centroids.shape[-1]
     kn = kc.shape[2]
     out = torch.empty(b, h, qn, kn, dtype=torch.bfloat16, device=qc.device)
     _lib.call("svoo_centroid_scores", qc.contiguous().data_ptr(), kc.contiguous().data_ptr(), b * h, qn, kn, d,
@@ -379,8 +382,8 @@ def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate
     """
     assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
     assert q.dtype == k.dtype == v.dtype, "Input dtypes must match"
-    in_dtype = q.dtype
-    q, k, v = (_lib.as_bf16(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    in_dtype, hd = q.dtype, q.shape[-1]
+    q, k, v = (_lib.as_rows128(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     b, h, s, d = q.shape
     assert k.shape == q.shape and v.shape == q.shape, "q, k, v must share one shape"
     qn = qc_size.shape[-1]
@@ -401,11 +404,11 @@ def dynamic_block_sparse_fwd(q, k, v, dynamic_map, qc_size, kc_size, *, validate
     ws = _lib.workspace(L.svoo_vbsa_workspace_size(bh, s, qn, kn), dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if validate else None
     _lib.call("svoo_vbsa_fwd", qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), m.data_ptr(), qs.data_ptr(),
-              ks.data_ptr(), out.data_ptr(), bh, s, d, qn, kn, ws.data_ptr(), ws.numel(), _lib.ptr(status),
+              ks.data_ptr(), out.data_ptr(), bh, s, hd, qn, kn, ws.data_ptr(), ws.numel(), _lib.ptr(status),
               _lib.stream_of(dev))
     if validate and int(status.item()) != 0:
         raise AssertionError("cluster sizes of every head must sum to S (qc_size / kc_size)")
-    return _lib.convert(out.reshape(b, h, s, d), in_dtype)
+    return _lib.from_rows128(out.reshape(b, h, s, d), hd, in_dtype)
 
 
 def dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, qc_size, kc_size, q_sorted_idx, k_sorted_idx,
@@ -419,8 +422,8 @@ def dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, qc_size, kc_s
     """
     assert query.is_cuda and key.is_cuda and value.is_cuda, "Inputs must be CUDA tensors"
     assert query.dtype == key.dtype == value.dtype, "Input dtypes must match"
-    in_dtype = query.dtype
-    query, key, value = (_lib.as_bf16(t, n) for t, n in ((query, "query"), (key, "key"), (value, "value")))
+    in_dtype, hd = query.dtype, query.shape[-1]
+    query, key, value = (_lib.as_rows128(t, n) for t, n in ((query, "query"), (key, "key"), (value, "value")))
     b, h, s, d = query.shape
     assert key.shape == query.shape and value.shape == query.shape, "q, k, v must share one shape"
     qn = qc_size.shape[-1]
@@ -441,11 +444,11 @@ def dynamic_block_sparse_fwd_fused(query, key, value, dynamic_map, qc_size, kc_s
     ws = _lib.workspace(L.svoo_vbsa_workspace_size(bh, s, qn, kn), dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if validate else None
     _lib.call("svoo_vbsa_fused_fwd", qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), qi.data_ptr(), ki.data_ptr(),
-              m.data_ptr(), qs.data_ptr(), ks.data_ptr(), out.data_ptr(), bh, h, s, d, qn, kn, ws.data_ptr(),
+              m.data_ptr(), qs.data_ptr(), ks.data_ptr(), out.data_ptr(), bh, h, s, hd, qn, kn, ws.data_ptr(),
               ws.numel(), _lib.ptr(status), _lib.stream_of(dev))
     if validate and int(status.item()) != 0:
         raise AssertionError("cluster sizes of every head must sum to S (qc_size / kc_size)")
-    return _lib.convert(out, in_dtype)
+    return _lib.from_rows128(out.view(b, s, h, d), hd, in_dtype).reshape(b, s, h * hd)
 
 
 def dynamic_block_sparse_fwd_flashinfer(q, k, v, block_mask_map, block_row_sz, block_col_sz, is_cpu: bool = True):

@@ -260,7 +260,7 @@ extern "C" int svoo_centroid_update(const uint16_t* x, const int32_t* sorted_idx
   SVOO_REQUIRE(x && sorted_idx && sorted_labels && sizes && old_c && new_c, SVOO_ERR_INVALID_ARG,
                "svoo_centroid_update: null pointer");
   SVOO_REQUIRE(bh > 0 && n > 0 && k > 0, SVOO_ERR_INVALID_ARG, "svoo_centroid_update: bad dims");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_centroid_update: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_centroid_update");
   SVOO_REQUIRE(bh <= 65535, SVOO_ERR_UNSUPPORTED, "svoo_centroid_update: bh too large");
   const size_t need = svoo_centroid_update_workspace_size(bh, k, d);
   SVOO_REQUIRE(workspace && ws_bytes >= need, SVOO_ERR_WORKSPACE, "svoo_centroid_update: workspace %zu < %zu",

@@ -1663,7 +1663,7 @@ static bool key_candidates_enabled(int qc, int kc) {
 extern "C" int svoo_cocluster_prep(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uint16_t* e_lo,
                                    float* profile, int bh, int j, int kp, int d, int jpad, void* stream) {
   SVOO_REQUIRE(a && b && e_hi && e_lo, SVOO_ERR_INVALID_ARG, "svoo_cocluster_prep: null pointer");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_cocluster_prep: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_cocluster_prep");
   SVOO_REQUIRE(bh > 0 && bh <= 65535 && j > 0 && kp > 0, SVOO_ERR_INVALID_ARG, "svoo_cocluster_prep: bad dims");
   SVOO_REQUIRE(j <= kMaxClusters && kp <= kMaxClusters, SVOO_ERR_UNSUPPORTED,
                "svoo_cocluster_prep: cluster counts above %d", kMaxClusters);
@@ -1675,7 +1675,7 @@ extern "C" int svoo_cocluster_prep(const uint16_t* a, const uint16_t* b, uint16_
 extern "C" int svoo_cocluster_assign(const uint16_t* x, const uint16_t* e_hi, const uint16_t* e_lo, int32_t* labels,
                                      int bh, int n, int j, int jpad, int d, void* stream) {
   SVOO_REQUIRE(x && e_hi && e_lo && labels, SVOO_ERR_INVALID_ARG, "svoo_cocluster_assign: null pointer");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_cocluster_assign: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_cocluster_assign");
   SVOO_REQUIRE(bh > 0 && bh <= 65535 && n > 0 && j > 0, SVOO_ERR_INVALID_ARG, "svoo_cocluster_assign: bad dims");
   SVOO_REQUIRE(jpad >= j && jpad % kAssignChunk == 0, SVOO_ERR_INVALID_ARG,
                "svoo_cocluster_assign: jpad=%d must be >= j and a multiple of %d", jpad, kAssignChunk);
@@ -1765,7 +1765,7 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   SVOO_REQUIRE(q && k && q_cent && k_cent && q_labels && k_labels && q_sizes && k_sizes && q_sorted_idx &&
                    k_sorted_idx && q_offsets && k_offsets,
                SVOO_ERR_INVALID_ARG, "svoo_co_cluster: null pointer");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_co_cluster: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_co_cluster");
   SVOO_REQUIRE(bh > 0 && bh <= 65535 && n > 0 && qc > 0 && kc > 0, SVOO_ERR_INVALID_ARG,
                "svoo_co_cluster: bad dims bh=%d n=%d qc=%d kc=%d", bh, n, qc, kc);
   SVOO_REQUIRE(qc <= kMaxClusters && kc <= kMaxClusters, SVOO_ERR_UNSUPPORTED,

@@ -113,7 +113,6 @@ __global__ void __launch_bounds__(kEarThreads) ear_value_kernel(const uint16_t* 
 // in both operands, so every lane loads 128 contiguous bytes of its row.
 constexpr int kEffClusters = 8;
 constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
-constexpr double kInvSqrtD = 0.08838834764831845;  // 128^-1/2
 
 // expm1(x) for |x| <= 0.1 by its Taylor series to x^4 (truncation below 1e-6 relative); beyond
 // 0.1 the difference e^a - e^c itself loses at most 6e-8 / 0.1 relative in fp32.
@@ -129,7 +128,7 @@ __global__ void __launch_bounds__(kEarThreads) ear_efficiency_kernel(
     const uint16_t* __restrict__ qc, const uint16_t* __restrict__ kp, const uint16_t* __restrict__ clog,
     const float2* __restrict__ tok_stats, const float* __restrict__ vc_sq, const int32_t* __restrict__ qs,
     const int32_t* __restrict__ ks, const int32_t* __restrict__ koff, int n, int qn, int kn, float scale2,
-    float gamma, float log_eps, float eps, float* __restrict__ eff) {
+    double inv_sqrt_d, float gamma, float log_eps, float eps, float* __restrict__ eff) {
   const int b = blockIdx.y, j0 = blockIdx.x * kEffClusters;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave, h = lane / 32, l32 = lane % 32;
   const int j1 = min(kn, j0 + kEffClusters);
@@ -181,7 +180,7 @@ __global__ void __launch_bounds__(kEarThreads) ear_efficiency_kernel(
             }
           }
           dot += __shfl_xor(dot, 32);
-          x_single = (float)(dot * kInvSqrtD - (double)c);
+          x_single = (float)(dot * inv_sqrt_d - (double)c);
         }
         // token statistics of this lane's 16 tokens, loaded with the K rows (clamped rows are masked below)
         float2 sv[16];
@@ -409,7 +408,7 @@ extern "C" int svoo_ear_value_stats(const uint16_t* v_perm, const int32_t* k_off
                                     float* tok_stats, void* stream) {
   SVOO_REQUIRE(v_perm && k_offsets && k_sizes && v_cent && vc_sq && tok_stats, SVOO_ERR_INVALID_ARG,
                "svoo_ear_value_stats: null pointer");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_ear_value_stats: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_ear_value_stats");
   SVOO_REQUIRE(bh > 0 && n > 0 && kn > 0 && bh <= 65535, SVOO_ERR_INVALID_ARG, "svoo_ear_value_stats: bad dims");
   hipLaunchKernelGGL(ear_value_kernel, dim3(kn, bh), dim3(kEarThreads), 0, (hipStream_t)stream, v_perm, k_offsets,
                      k_sizes, n, kn, compute_vc, v_cent, vc_sq, (float2*)tok_stats);
@@ -419,7 +418,7 @@ extern "C" int svoo_ear_value_stats(const uint16_t* v_perm, const int32_t* k_off
 extern "C" int svoo_ear_centroid_logits(const uint16_t* qc, const uint16_t* kc, int bh, int qn, int kn, int d,
                                         uint16_t* c_logits, void* stream) {
   SVOO_REQUIRE(qc && kc && c_logits, SVOO_ERR_INVALID_ARG, "svoo_ear_centroid_logits: null pointer");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_ear_centroid_logits: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_ear_centroid_logits");
   SVOO_REQUIRE(bh > 0 && qn > 0 && kn > 0 && bh <= 65535 && qn <= 65535, SVOO_ERR_INVALID_ARG,
                "svoo_ear_centroid_logits: bad dims");
   // c_ij = bf16(bf16(qc_i . kc_j) * f32(D^-1/2)): the centroid scores of the block mask
@@ -432,14 +431,14 @@ extern "C" int svoo_ear_efficiency(const uint16_t* qc, const uint16_t* k_perm, c
                                    int d, float gamma, float eps, float* eff, void* stream) {
   SVOO_REQUIRE(qc && k_perm && c_logits && tok_stats && vc_sq && q_sizes && k_sizes && k_offsets && eff,
                SVOO_ERR_INVALID_ARG, "svoo_ear_efficiency: null pointer");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_ear_efficiency: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_ear_efficiency");
   SVOO_REQUIRE(bh > 0 && n > 0 && qn > 0 && kn > 0 && bh <= 65535 && eps > 0.0f, SVOO_ERR_INVALID_ARG,
                "svoo_ear_efficiency: bad dims");
   const float scale2 = (float)(1.4426950408889634 / sqrt((double)d));  // log2(e) / sqrt(D)
   dim3 grid((kn + kEffClusters - 1) / kEffClusters, bh);
   hipLaunchKernelGGL(ear_efficiency_kernel, grid, dim3(kEarThreads), 0, (hipStream_t)stream, qc, k_perm, c_logits,
-                     (const float2*)tok_stats, vc_sq, q_sizes, k_sizes, k_offsets, n, qn, kn, scale2, gamma,
-                     logf(eps), eps, eff);
+                     (const float2*)tok_stats, vc_sq, q_sizes, k_sizes, k_offsets, n, qn, kn, scale2,
+                     1.0 / sqrt((double)d), gamma, logf(eps), eps, eff);
   return check_launch("svoo_ear_efficiency");
 }
 

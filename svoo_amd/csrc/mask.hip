@@ -546,7 +546,7 @@ extern "C" int svoo_centroid_scores(const uint16_t* qc, const uint16_t* kc, int 
                                     uint16_t* scores, void* stream) {
   SVOO_REQUIRE(qc && kc && scores, SVOO_ERR_INVALID_ARG, "svoo_centroid_scores: null pointer");
   SVOO_REQUIRE(bh > 0 && qn > 0 && kn > 0, SVOO_ERR_INVALID_ARG, "svoo_centroid_scores: bad dims");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_centroid_scores: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_centroid_scores");
   SVOO_REQUIRE(bh <= 65535 && kn <= (1 << 26), SVOO_ERR_UNSUPPORTED, "svoo_centroid_scores: grid too large");
   const float inv = 1.0f / (float)sqrt((double)d);
   hipLaunchKernelGGL(centroid_scores_kernel, dim3((kn + 31) / 32, bh), dim3(kScoreThreads), 0, (hipStream_t)stream,
@@ -561,7 +561,7 @@ extern "C" int svoo_block_mask(const uint16_t* qc, const uint16_t* kc, const int
   SVOO_REQUIRE(map && (full || (qc && kc && k_sizes && preserve && cap && scores)), SVOO_ERR_INVALID_ARG,
                "svoo_block_mask: null pointer");
   SVOO_REQUIRE(b > 0 && h > 0 && qn > 0 && kn > 0, SVOO_ERR_INVALID_ARG, "svoo_block_mask: bad dims");
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "svoo_block_mask: D=%d (only 128 supported)", d);
+  SVOO_REQUIRE_HEAD_DIM(d, "svoo_block_mask");
   SVOO_REQUIRE(kn <= 4096, SVOO_ERR_UNSUPPORTED, "svoo_block_mask: Kc=%d exceeds 4096", kn);
   SVOO_REQUIRE(qn <= 65535 && (long long)b * h <= 65535, SVOO_ERR_UNSUPPORTED, "svoo_block_mask: grid too large");
   dim3 grid(qn, b * h);

@@ -189,3 +189,8 @@ int check_launch(const char* what);
       return (code);                      \
     }                                     \
   } while (0)
+
+// Head dims: rows always hold 128 elements; d (1..128) is the head dim, elements d..127 of every row are zero.
+#define SVOO_REQUIRE_HEAD_DIM(d, name)                                                                    \
+  SVOO_REQUIRE((d) >= 1 && (d) <= 128, SVOO_ERR_UNSUPPORTED, "%s: D=%d (head dims 1..128, rows of 128)", \
+               name, (d))

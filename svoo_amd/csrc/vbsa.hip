@@ -965,7 +965,7 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
                 void* stream, const int32_t* q_idx = nullptr, const int32_t* k_idx = nullptr, int heads = 1) {
   SVOO_REQUIRE(q && k && v && map && q_sizes && k_sizes && o && (!EAR || (kc && vc)), SVOO_ERR_INVALID_ARG,
                "%s: null pointer", name);
-  SVOO_REQUIRE(d == 128, SVOO_ERR_UNSUPPORTED, "%s: D=%d (only 128 supported)", name, d);
+  SVOO_REQUIRE_HEAD_DIM(d, name);
   SVOO_REQUIRE(bh > 0 && s > 0 && qn > 0 && kn > 0, SVOO_ERR_INVALID_ARG, "%s: bad dims", name);
   SVOO_REQUIRE(kn <= kMaxKN && qn < 32768, SVOO_ERR_UNSUPPORTED, "%s: qn=%d kn=%d above limits", name, qn, kn);
   SVOO_REQUIRE((long long)bh * s * 128 < (1ll << 40), SVOO_ERR_UNSUPPORTED, "%s: too large", name);

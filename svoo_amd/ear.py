@@ -39,11 +39,11 @@ EAR_EPS = 1e-8  # identify_dynamic_map_estimated's eps (svoo/co_clustering.py:17
 
 
 def _bf16_4d(x: torch.Tensor, name: str) -> torch.Tensor:
-    """``x [B, H, N, 128]`` as the kernels' bf16 operand (fp16 / fp32 rounded to bf16, to nearest even)."""
-    xx = _lib.as_bf16(x, name)
-    if xx.dim() != 4 or xx.shape[-1] != 128:
-        raise ValueError(f"{name}: expected [B, H, N, 128], got {tuple(x.shape)}")
-    return xx.contiguous()
+    """``x [B, H, N, D]`` (D <= 128) as the kernels' bf16 operand ``[B, H, N, 128]`` (fp16 / fp32 rounded to bf16,
+    to nearest even; columns past D zero)."""
+    if isinstance(x, torch.Tensor) and x.dim() != 4:
+        raise ValueError(f"{name}: expected [B, H, N, D], got {tuple(x.shape)}")
+    return _lib.as_rows128(x, name).contiguous()
 
 
 def _sizes(x: torch.Tensor, dev, bh: int, n: int) -> torch.Tensor:
@@ -106,7 +106,7 @@ def value_centroids_from_permuted(v_perm: torch.Tensor, k_cluster_sizes: torch.T
     kn = k_cluster_sizes.shape[-1]
     ks = _sizes(k_cluster_sizes, vp.device, b * h, kn)
     vc, _, _ = _value_stats(vp.reshape(b * h, s, d), ks, _offsets(ks), None)
-    return _lib.convert(vc.reshape(b, h, kn, d), v_perm.dtype)
+    return _lib.from_rows128(vc.reshape(b, h, kn, d), v_perm.shape[-1], v_perm.dtype)
 
 
 def compute_value_centroids(tokens: torch.Tensor, labels: torch.Tensor, cluster_sizes: torch.Tensor,
@@ -129,23 +129,28 @@ def compute_value_centroids(tokens: torch.Tensor, labels: torch.Tensor, cluster_
 def centroid_logits(query_centroids: torch.Tensor, key_centroids: torch.Tensor) -> torch.Tensor:
     """``einsum("bhqd,bhkd->bhqk", Qc, Kc) * D**-0.5`` on bf16 centroids (``co_clustering.py:1725``):
     the exact dot rounded to bf16, times ``float32(D**-0.5)``, rounded to bf16."""
-    qc = _bf16_4d(query_centroids, "query_centroids")
-    kc = _bf16_4d(key_centroids, "key_centroids")
-    b, h, qn, d = qc.shape
-    kn = kc.shape[2]
-    c = torch.empty(b, h, qn, kn, dtype=torch.bfloat16, device=qc.device)
-    _lib.call("svoo_ear_centroid_logits", qc.data_ptr(), kc.data_ptr(), b * h, qn, kn, d, c.data_ptr(),
-              _lib.stream_of(qc.device))
+    c = _centroid_logits(_bf16_4d(query_centroids, "query_centroids"), _bf16_4d(key_centroids, "key_centroids"),
+                         query_centroids.shape[-1])
     return _lib.convert(c, query_centroids.dtype)
 
 
-def _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma: float, eps: float) -> torch.Tensor:
-    b, h, qn, d = qc.shape
+def _centroid_logits(qc: torch.Tensor, kc: torch.Tensor, hd: int) -> torch.Tensor:
+    """The bf16 logits of padded centroids ``[B, H, *, 128]`` with the scale of head dim ``hd``."""
+    b, h, qn, _ = qc.shape
+    kn = kc.shape[2]
+    c = torch.empty(b, h, qn, kn, dtype=torch.bfloat16, device=qc.device)
+    _lib.call("svoo_ear_centroid_logits", qc.data_ptr(), kc.data_ptr(), b * h, qn, kn, hd, c.data_ptr(),
+              _lib.stream_of(qc.device))
+    return c
+
+
+def _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma: float, eps: float, hd: int) -> torch.Tensor:
+    b, h, qn, _ = qc.shape
     n = kp.shape[2]
     kn = ks.shape[-1]
     eff = torch.empty(b, h, qn, kn, dtype=torch.float32, device=qc.device)
     _lib.call("svoo_ear_efficiency", qc.data_ptr(), kp.data_ptr(), c.contiguous().data_ptr(), stats.data_ptr(),
-              vc_sq.data_ptr(), qs.data_ptr(), ks.data_ptr(), koff.data_ptr(), b * h, n, qn, kn, d, float(gamma),
+              vc_sq.data_ptr(), qs.data_ptr(), ks.data_ptr(), koff.data_ptr(), b * h, n, qn, kn, hd, float(gamma),
               float(eps), eff.data_ptr(), _lib.stream_of(qc.device))
     return eff
 
@@ -168,7 +173,7 @@ def error_estimation_triton(query_centroids, key_centroids, value_centroids, per
     vc = _bf16_4d(value_centroids, "value_centroids")
     _, vc_sq, stats = _value_stats(vp.reshape(b * h, s, d), ks, koff, vc)
     c = _lib.as_bf16(c_logits, "c_logits").contiguous()
-    return _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma, eps)
+    return _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma, eps, query_centroids.shape[-1])
 
 
 # ------------------------------------------------------------------------------------------------ selection
@@ -202,10 +207,11 @@ def identify_dynamic_map_estimated(q_perm, k_perm, v_perm, qc_sz, kc_sz, qcentro
     ks = _sizes(kc_sz, dev, b * h, kn)
     qs = _sizes(qc_sz, dev, b * h, qn)
     koff = _offsets(ks)
-    c = centroid_logits(qc, kcentroids)
+    hd = qcentroids.shape[-1]
+    c = _centroid_logits(qc, _bf16_4d(kcentroids, "kcentroids"), hd)
     vc = _bf16_4d(vcentroids, "vcentroids")
     _, vc_sq, stats = _value_stats(vp.reshape(b * h, s, d), ks, koff, vc)
-    eff = _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma, EAR_EPS)
+    eff = _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma, EAR_EPS, hd)
     return _select(c, eff, qs, ks, b, h, qn, kn, top_p, min_kc_ratio)
 
 
@@ -224,10 +230,11 @@ def ear_map_and_value_centroids(q_perm, k_perm, v_perm, qc_sz, kc_sz, qcentroids
     qs = _sizes(qc_sz, dev, b * h, qn)
     koff = _offsets(ks)
     vc, vc_sq, stats = _value_stats(vp.reshape(b * h, s, d), ks, koff, None)
-    c = centroid_logits(qc, kcentroids)
-    eff = _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma, EAR_EPS)
+    hd = qcentroids.shape[-1]
+    c = _centroid_logits(qc, _bf16_4d(kcentroids, "kcentroids"), hd)
+    eff = _efficiency(qc, kp, c, stats, vc_sq, qs, ks, koff, gamma, EAR_EPS, hd)
     dmap = _select(c, eff, qs, ks, b, h, qn, kn, top_p, min_kc_ratio)
-    vc = _lib.convert(vc.reshape(b, h, kn, d), v_perm.dtype)
+    vc = _lib.from_rows128(vc.reshape(b, h, kn, d), v_perm.shape[-1], v_perm.dtype)
     if return_parts:
         return vc, dmap, {"c": c, "eff": eff}
     return vc, dmap
@@ -244,14 +251,15 @@ def dynamic_block_sparse_prune_fwd(q, k, v, k_centroids, v_centroids, block_mask
     are checked before the launch, and without ``validate`` inconsistent device sizes give NaN rows."""
     assert q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be CUDA tensors"
     assert q.dtype == k.dtype == v.dtype, "Input dtypes must match"
-    in_dtype = q.dtype
-    q, k, v = (_lib.as_bf16(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    in_dtype, hd = q.dtype, q.shape[-1]
+    assert k_centroids.shape[-1] == hd and v_centroids.shape[-1] == hd, "centroids must have the head dim of q"
+    q, k, v = (_lib.as_rows128(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     b, h, s, d = q.shape
     qn = block_row_sz.shape[-1]
     kn = block_col_sz.shape[-1]
     assert k.shape == q.shape and v.shape == q.shape, "q, k, v must share one shape"
     assert block_mask_map.shape == (b, h, qn, kn)
-    assert k_centroids.shape == (b, h, kn, d) and v_centroids.shape == (b, h, kn, d)
+    assert k_centroids.shape == (b, h, kn, hd) and v_centroids.shape == (b, h, kn, hd)
     _check_host_sizes(block_row_sz, s, "block_row_sz")
     _check_host_sizes(block_col_sz, s, "block_col_sz")
     dev = q.device
@@ -267,11 +275,11 @@ def dynamic_block_sparse_prune_fwd(q, k, v, k_centroids, v_centroids, block_mask
     ws = _lib.workspace(L.svoo_vbsa_workspace_size(bh, s, qn, kn), dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev) if validate else None
     _lib.call("svoo_vbsa_ear_fwd", qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-              m.data_ptr(), qs.data_ptr(), ks.data_ptr(), out.data_ptr(), bh, s, d, qn, kn, ws.data_ptr(), ws.numel(),
+              m.data_ptr(), qs.data_ptr(), ks.data_ptr(), out.data_ptr(), bh, s, hd, qn, kn, ws.data_ptr(), ws.numel(),
               _lib.ptr(status), _lib.stream_of(dev))
     if validate and int(status.item()) != 0:
         raise AssertionError("cluster sizes of every head must sum to S (block_row_sz / block_col_sz)")
-    return _lib.convert(out.reshape(b, h, s, d), in_dtype)
+    return _lib.from_rows128(out.reshape(b, h, s, d), hd, in_dtype)
 
 
 def dynamic_block_sparse_prune_fwd_flashinfer(q, k, v, k_centroids, v_centroids, block_mask_map, block_row_sz,

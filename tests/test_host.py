@@ -37,12 +37,14 @@ def test_library_reports_errors_without_launching():
     assert L.svoo_version() == 100
     rc = L.svoo_vbsa_fwd(None, None, None, None, None, None, None, 1, 1, 128, 1, 1, None, 0, None, None)
     assert rc == -1 and "null pointer" in _lib.last_error()
-    rc = L.svoo_block_mask(1, 1, 1, 1, 1, 1, 1, 1, 1, 64, 0.5, 0, 1, None, 1, None)
-    assert rc == -2 and "D=64" in _lib.last_error()
+    rc = L.svoo_block_mask(1, 1, 1, 1, 1, 1, 1, 1, 1, 160, 0.5, 0, 1, None, 1, None)
+    assert rc == -2 and "D=160" in _lib.last_error()
     rc = L.svoo_block_mask(1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 0.5, 0, 1, None, None, None)
     assert rc == -1 and "null pointer" in _lib.last_error()  # the scores buffer is required
-    rc = L.svoo_centroid_scores(1, 1, 1, 1, 1, 64, 1, None)
-    assert rc == -2 and "D=64" in _lib.last_error()
+    rc = L.svoo_centroid_scores(1, 1, 1, 1, 1, 0, 1, None)
+    assert rc == -2 and "D=0" in _lib.last_error()
+    rc = L.svoo_convert_rows(1, 0, 0, 1, 0, 128, 4, None)
+    assert rc == -1 and "src_cols=0" in _lib.last_error()
     assert L.svoo_co_cluster_workspace_size(40, 75600, 100, 1000, 128) > 0
     rc = L.svoo_convert(1, 0, 1, 3, 8, None)
     assert rc == -1 and "element types" in _lib.last_error()
@@ -65,6 +67,8 @@ def test_operators_reject_non_float_inputs_before_any_call():
         _lib.as_bf16(torch.zeros(2, 3, 128), "x")  # a float tensor on the CPU
     with pytest.raises(AssertionError, match="CUDA"):
         dynamic_block_sparse_fwd(*(torch.zeros(1, 1, 8, 128),) * 3, None, None, None)
+    with pytest.raises(ValueError, match="head dim 192"):
+        _lib.as_rows128(torch.zeros(2, 3, 192), "x")
 
 
 def test_noalloc_attention_rejects_plans_above_its_scratch():
