@@ -115,17 +115,18 @@ def _bf(shape, seed, dev):
     return x, torch.from_numpy(x).to(torch.bfloat16).to(dev)
 
 
-def test_hunyuan_sparse_call_matches_oracle(gpu):
-    say("hunyuan attention_core_logic sparse")
+@pytest.mark.parametrize("d", [128, 64])
+def test_hunyuan_sparse_call_matches_oracle(gpu, d):
+    say("hunyuan attention_core_logic sparse, head dim", d)
     from svoo_amd import synth
 
     # video tokens from the seeded Gaussian mixture (well separated: labels agree with the oracle),
     # text tokens appended
-    cfg = synth.SynthConfig("hy-small", 41, 2, 2, 12, 16, 128, 24, 12, 24, 3, 0.1, 0.4, True, "bf16")
+    cfg = synth.SynthConfig("hy-small", 41, 2, 2, 12, 16, d, 24, 12, 24, 3, 0.1, 0.4, True, "bf16")
     h, frames, fsize, ctx, prompt = cfg.heads, cfg.frames, cfg.frame_size, 32, 20
     s = frames * fsize + ctx
     vids = synth.make_qkv(cfg)
-    txt = [_bf((1, h, ctx, 128), seed, gpu)[0] for seed in (1, 2, 3)]
+    txt = [_bf((1, h, ctx, d), seed, gpu)[0] for seed in (1, 2, 3)]
     full = [np.concatenate([vt_.float().numpy(), tx], axis=2) for vt_, tx in zip(vids, txt)]
     q, k, v = full
     qt, kt, vt = (torch.from_numpy(a).to(torch.bfloat16).to(gpu) for a in full)
@@ -138,7 +139,7 @@ def test_hunyuan_sparse_call_matches_oracle(gpu):
     out = proc.attention_core_logic(qt, kt, vt, torch.tensor([100.0], device=gpu), 0)
     torch.cuda.synchronize()
     ref = O.hunyuan_attention_call(q, k, v, 12, 24, 3, 0.9, ratios, prompt, ctx, init_q_idx=qi, init_k_idx=ki)
-    assert out.shape == (1, h, s, 128)
+    assert out.shape == (1, h, s, d)
     check(out, ref)
 
 
