@@ -148,25 +148,58 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
   }
 }
 
-// Launch order of the heads: by work, heaviest first (ties by index), so the last work items of the
-// grid are short ones.  bh above kOrderMax keeps the natural order.
+// The grid's work list.  Heads in launch order: by work, heaviest first (ties by index), so the last work
+// items of the grid are short ones (bh above kOrderMax keeps the natural order).  The list holds, head after
+// head in that order, one entry (head << 15 | item slot) per work item of the head: its nitems slots, or for a
+// head whose sizes do not sum to S one NaN-filling slot per qtile token rows; -1 fills the rest of its
+// bh * cap entries.  A dense list gives every XCD an equal share of the real items: with per-head slot ranges
+// the unused slots at the end of each head's range fall on the same XCDs head after head.
 constexpr int kOrderMax = 4096;
-__global__ void __launch_bounds__(kPlanThreads) vbsa_order_kernel(const int32_t* __restrict__ work, int bh,
-                                                                  int32_t* __restrict__ order) {
-  __shared__ int32_t w[kOrderMax];
+__global__ void __launch_bounds__(kPlanThreads) vbsa_order_kernel(const int32_t* __restrict__ work,
+                                                                  const int32_t* __restrict__ nitems, int bh, int cap,
+                                                                  int nan_slots, int32_t* __restrict__ list) {
+  __shared__ int32_t w[kOrderMax], rk[kOrderMax];  // work and rank of each head, then the head of each rank
+  __shared__ long long red[kPlanThreads / kWave];
+  __shared__ int32_t c_head[kPlanThreads], c_n[kPlanThreads], c_base[kPlanThreads];
   const int tid = threadIdx.x;
-  if (bh > kOrderMax) {
-    for (int h = tid; h < bh; h += kPlanThreads) order[h] = h;
-    return;
+  const bool ranked = bh <= kOrderMax;
+  if (ranked) {
+    for (int h = tid; h < bh; h += kPlanThreads) w[h] = work[h];
+    __syncthreads();
+    for (int h = tid; h < bh; h += kPlanThreads) {
+      const int wh = w[h];
+      int rank = 0;
+      for (int g = 0; g < bh; ++g) rank += (w[g] > wh || (w[g] == wh && g < h)) ? 1 : 0;
+      rk[h] = rank;
+    }
+    __syncthreads();  // every thread is done reading the work values
+    for (int h = tid; h < bh; h += kPlanThreads) w[rk[h]] = h;
+    __syncthreads();
   }
-  for (int h = tid; h < bh; h += kPlanThreads) w[h] = work[h];
-  __syncthreads();
-  for (int h = tid; h < bh; h += kPlanThreads) {
-    const int wh = w[h];
-    int rank = 0;
-    for (int g = 0; g < bh; ++g) rank += (w[g] > wh || (w[g] == wh && g < h)) ? 1 : 0;
-    order[rank] = h;
+  long long run = 0;
+  for (int r0 = 0; r0 < bh; r0 += kPlanThreads) {
+    const int r = r0 + tid;
+    int n = 0, h = 0;
+    if (r < bh) {
+      h = ranked ? w[r] : r;
+      const int ni = nitems[h];
+      n = ni >= 0 ? ni : nan_slots;
+    }
+    long long tot;
+    const long long ex = block_exclusive_scan_i64<kPlanThreads>(n, red, &tot);
+    c_head[tid] = h;
+    c_n[tid] = n;
+    c_base[tid] = (int32_t)(run + ex);
+    __syncthreads();
+    const int m = min(kPlanThreads, bh - r0);
+    for (int i = 0; i < m; ++i) {
+      const int32_t tag = c_head[i] << 15, base = c_base[i];
+      for (int j = tid; j < c_n[i]; j += kPlanThreads) list[base + j] = tag | j;
+    }
+    __syncthreads();  // the chunk's tables are read before the next chunk writes them
+    run += tot;
   }
+  for (long long i = run + tid; i < (long long)bh * cap; i += kPlanThreads) list[i] = -1;
 }
 
 // Compacts the active key clusters of one map row into (start, cumulative length) segments in
@@ -280,12 +313,16 @@ __device__ __forceinline__ int cursor_row(KvCursor& c, const int32_t* seg_start,
 // from different groups and alternate between an MFMA phase M(t) = {O += V(t)^T P(t)^T, S(t+1) =
 // K(t+1) Q^T} and a VALU phase V(t) = {softmax of S(t) -> P(t)}; group B runs one half-step behind
 // group A, so in every half-step one wave per SIMD does MFMA work while the other does VALU work.
-// Group B also issues the LDS DMA of the next K/V tiles and resolves their token rows.
+// Group B also issues the LDS DMA of the next K/V tiles; waves 0 and 1 resolve their token rows into
+// the row tables during group A's softmax half-step.
 // Half items (HC kernels only: a second set of K/V buffers in LDS): a last tile of at most 128
 // queries is taken by both groups, each wave of a group holding the same 32 queries as its partner
 // in the other group; group A walks the even tiles of the KV stream (stream 0), group B the odd
 // ones (stream 1), on the same half-step schedule, and the two online-softmax states are merged
-// through LDS at the end, so such an item costs about half the time of a full one.
+// through LDS at the end, so such an item costs about half the time of a full one.  Each group copies
+// its own stream's tiles during its softmax, and group A's waves resolve the four row tables (one
+// each) at the start of their MFMA half-step, where they would otherwise wait at the barrier for
+// group B's longer softmax with copies.
 template <int QB, bool EAR, bool IDX, bool HC>
 __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) vbsa_attn_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -294,7 +331,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     int cap, long long total_items, const int32_t* __restrict__ qoff, const int32_t* __restrict__ koff,
     const int32_t* __restrict__ items, const int32_t* __restrict__ nitems, float scale_log2,
     const int32_t* __restrict__ q_idx, const int32_t* __restrict__ k_idx, int heads,
-    const int32_t* __restrict__ order) {
+    const int32_t* __restrict__ list) {
   constexpr int kQTile = VbsaCfg<QB>::kQTile;
   constexpr int kThreads = kVWaves * kWave;
   constexpr int kDmaIt = kKT / (4 * 4);  // 4-row DMA groups per group-B wave per tile and matrix
@@ -309,23 +346,21 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
 
   const long long item = xcd_item(blockIdx.x);
   if (item >= total_items) return;
-  const int b = order[(int)(item / cap)], local = (int)(item % cap);
-  const int head_items = nitems[b];
-  if (local >= head_items) {
-    if (head_items < 0 && (long long)local * kQTile < s) {
-      // Sizes of this head do not sum to S (the reference asserts, svoo/co_clustering.py:1138-1139):
-      // item slot `local` writes NaN over token rows [local * kQTile, +kQTile) of the head, so the
-      // failure is visible in the output instead of leaving the buffer's old contents.  cap >=
-      // ceil(S / kQTile), so the slots cover every row.  Rows are addressed by token (not through
-      // the sorted indices, which may be as inconsistent as the sizes).
-      const int r0 = local * kQTile, r1 = min(s, r0 + kQTile);
-      const u32x4_t nan4 = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
-      for (int idx = threadIdx.x; idx < (r1 - r0) * 16; idx += kVWaves * kWave) {
-        const int t = r0 + idx / 16;
-        uint16_t* row = IDX ? o + (((size_t)(b / heads) * s + t) * heads + (b % heads)) * 128
-                            : o + ((size_t)b * s + t) * 128;
-        ((u32x4_t*)row)[idx % 16] = nan4;
-      }
+  const int32_t entry = list[item];
+  if (entry < 0) return;  // past the last work item
+  const int b = entry >> 15, local = entry & 0x7fff;
+  if (nitems[b] < 0) {
+    // Sizes of this head do not sum to S (the reference asserts, svoo/co_clustering.py:1138-1139):
+    // slot `local` (one of ceil(S / kQTile)) writes NaN over token rows [local * kQTile, +kQTile) of the
+    // head, so the failure is visible in the output instead of leaving the buffer's old contents.  Rows
+    // are addressed by token (not through the sorted indices, which may be as inconsistent as the sizes).
+    const int r0 = local * kQTile, r1 = min(s, r0 + kQTile);
+    const u32x4_t nan4 = {0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u};
+    for (int idx = threadIdx.x; idx < (r1 - r0) * 16; idx += kVWaves * kWave) {
+      const int t = r0 + idx / 16;
+      uint16_t* row = IDX ? o + (((size_t)(b / heads) * s + t) * heads + (b % heads)) * 128
+                          : o + ((size_t)b * s + t) * 128;
+      ((u32x4_t*)row)[idx % 16] = nan4;
     }
     return;
   }
@@ -405,14 +440,14 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   float m_run = -INFINITY, l_run = 0.0f;
 
   // Row tables (lane = tile position): in a full item wave 0 resolves K tiles and wave 1 V tiles; in a
-  // half item waves 4 and 5 resolve stream 0 (even tiles), waves 6 and 7 stream 1 (odd tiles).
+  // half item waves 0 and 1 resolve stream 0 (even tiles), waves 2 and 3 stream 1 (odd tiles).
   // Rows past the stream repeat its last token row (0 when an EAR row has no active tokens); EAR
   // centroid j of the K (V) table is row crow_k + j (crow_v + j).
   int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
   if constexpr (IDX) last_row = kix[last_row];
   KvCursor cursor;
-  const bool resolver = (half ? wave >= 4 : wave < 2) && nseg > 0;
-  const int p_first = (half && wave >= 6 ? kKT : 0) + lane;  // this lane's row in the wave's first tile
+  const bool resolver = (half ? wave < 4 : wave < 2) && nseg > 0;
+  const int p_first = (half && wave >= 2 ? kKT : 0) + lane;  // this lane's row in the wave's first tile
   if (resolver) cursor_init(cursor, seg_start, seg_cum, nseg, min(p_first, total_tok - 1));
   // IDX: the token index of this lane's row in the next tile the wave resolves, loaded one call
   // ahead so that the global load's latency is off the resolving wave's path
@@ -735,14 +770,14 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   } else if constexpr (HC) {
     // Half item: local tile u of stream x is global tile 2u + x; stream 0 (n0 tiles) lives in the
     // k_s / v_s buffers and is used by group A, stream 1 (n1 tiles) in k1_s / v1_s, used by group B.
-    // Each group copies its own stream's tiles during its softmax; waves 4-7 resolve the four tables.
+    // Each group copies its own stream's tiles during its softmax; waves 0-3 resolve the four tables.
     const int n0 = (ntiles + 1) / 2, n1 = ntiles / 2;
-    // Tables of step u (waves 4-7, at the end of group B's softmax half-step): K(u+3) and V(u+2) of each stream.
+    // Tables of step u (waves 0-3, before group A's MFMA half-step): K(u+3) and V(u+2) of each stream.
     auto resolve2 = [&](int u) __attribute__((always_inline)) {
-      if (wave == 4 && u + 3 < n0) resolve(rowtab[0][0][(u + 1) & 1], 2 * (u + 3), 2);
-      if (wave == 5 && u + 2 < n0) resolve(rowtab[0][1][u & 1], 2 * (u + 2), 2);
-      if (wave == 6 && u + 3 < n1) resolve(rowtab[1][0][(u + 1) & 1], 2 * (u + 3) + 1, 2);
-      if (wave == 7 && u + 2 < n1) resolve(rowtab[1][1][u & 1], 2 * (u + 2) + 1, 2);
+      if (wave == 0 && u + 3 < n0) resolve(rowtab[0][0][(u + 1) & 1], 2 * (u + 3), 2);
+      if (wave == 1 && u + 2 < n0) resolve(rowtab[0][1][u & 1], 2 * (u + 2), 2);
+      if (wave == 2 && u + 3 < n1) resolve(rowtab[1][0][(u + 1) & 1], 2 * (u + 3) + 1, 2);
+      if (wave == 3 && u + 2 < n1) resolve(rowtab[1][1][u & 1], 2 * (u + 2) + 1, 2);
     };
     // Rows of the copies of K(u+2) and V(u+1) of a stream with n tiles (tables of slot u & 1 and (u + 1) & 1).
     // A tile past the stream takes row 0 of the head: the copy lands in a buffer that is not read for it.
@@ -750,19 +785,19 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       rk = u + 2 < n ? dma_rows(rowtab[x][0][u & 1]) : make_int4(0, 0, 0, 0);
       rv = u + 1 < n ? dma_rows(rowtab[x][1][(u + 1) & 1]) : make_int4(0, 0, 0, 0);
     };
-    if (wave == 4) {
+    if (wave == 0) {
       resolve(rowtab[0][0][0], 0, 2);
       if (n0 > 1) resolve(rowtab[0][0][1], 2, 2);
     }
-    if (wave == 5) {
+    if (wave == 1) {
       resolve(rowtab[0][1][0], 0, 2);
       if (n0 > 1) resolve(rowtab[0][1][1], 2, 2);
     }
-    if (wave == 6 && n1 > 0) {
+    if (wave == 2 && n1 > 0) {
       resolve(rowtab[1][0][0], 1, 2);
       if (n1 > 1) resolve(rowtab[1][0][1], 3, 2);
     }
-    if (wave == 7 && n1 > 0) {
+    if (wave == 3 && n1 > 0) {
       resolve(rowtab[1][1][0], 1, 2);
       if (n1 > 1) resolve(rowtab[1][1][1], 3, 2);
     }
@@ -787,8 +822,8 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
         scores(k1_s0);
       }
     }
-    if (wave == 4 && n0 > 2) resolve(rowtab[0][0][0], 4, 2);
-    if (wave == 6 && n1 > 2) resolve(rowtab[1][0][0], 5, 2);
+    if (wave == 0 && n0 > 2) resolve(rowtab[0][0][0], 4, 2);
+    if (wave == 2 && n1 > 2) resolve(rowtab[1][0][0], 5, 2);
     __syncthreads();
     //   A: h = 2u -> M(u), h = 2u+1 -> V(u+1) with the copies of stream 0's K(u+2), V(u+1) spread through it;
     //   B: h = 2u -> V(u) with the copies of stream 1's K(u+2), V(u+1) spread through it and the tables,
@@ -797,6 +832,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     for (int u = 0; u < n0; u += 2) {
       int4 rk, rv;
       if (!group_b) {
+        resolve2(u);
         if (active) mphase(u, v_s0, k_s1);
       } else {
         rows2(1, u, n1, rk, rv);
@@ -804,7 +840,6 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
           vphase(2 * u + 1, true, rk, k1_s0, rv, v1_s1);
         else
           dma_all(rk, k1_s0, rv, v1_s1);
-        resolve2(u);
       }
       __syncthreads();
       if (!group_b) {
@@ -819,6 +854,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
       __syncthreads();
       if (u + 1 >= n0) break;
       if (!group_b) {
+        resolve2(u + 1);
         if (active) mphase(u + 1, v_s1, k_s0);
       } else {
         rows2(1, u + 1, n1, rk, rv);
@@ -826,7 +862,6 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
           vphase(2 * u + 3, true, rk, k1_s1, rv, v1_s0);
         else
           dma_all(rk, k1_s1, rv, v1_s0);
-        resolve2(u + 1);
       }
       __syncthreads();
       if (!group_b) {
@@ -933,7 +968,7 @@ using namespace svoo;
 namespace {
 constexpr int kDefaultQB = 1;
 struct VbsaWs {
-  size_t qoff, koff, items, nitems, work, order, total;
+  size_t qoff, koff, items, nitems, work, list, total;
   int cap;
 };
 VbsaWs vbsa_layout(int bh, int s, int qn, int kn) {
@@ -946,8 +981,8 @@ VbsaWs vbsa_layout(int bh, int s, int qn, int kn) {
   w.items = w.koff + al((size_t)bh * (kn + 1) * 4);
   w.nitems = w.items + al((size_t)bh * w.cap * 4);
   w.work = w.nitems + al((size_t)bh * 4);
-  w.order = w.work + al((size_t)bh * 4);
-  w.total = w.order + al((size_t)bh * 4);
+  w.list = w.work + al((size_t)bh * 4);
+  w.total = w.list + al((size_t)bh * w.cap * 4);
   return w;
 }
 }  // namespace
@@ -968,6 +1003,8 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   SVOO_REQUIRE_HEAD_DIM(d, name);
   SVOO_REQUIRE(bh > 0 && s > 0 && qn > 0 && kn > 0, SVOO_ERR_INVALID_ARG, "%s: bad dims", name);
   SVOO_REQUIRE(kn <= kMaxKN && qn < 32768, SVOO_ERR_UNSUPPORTED, "%s: qn=%d kn=%d above limits", name, qn, kn);
+  // a work-list entry is head << 15 | slot
+  SVOO_REQUIRE(bh < 65536, SVOO_ERR_UNSUPPORTED, "%s: bh=%d above 65535", name, bh);
   SVOO_REQUIRE((long long)bh * s * 128 < (1ll << 40), SVOO_ERR_UNSUPPORTED, "%s: too large", name);
   SVOO_REQUIRE(s < (1 << 24), SVOO_ERR_UNSUPPORTED, "%s: S=%d above 2^24 tokens per head", name, s);
   const VbsaWs lay = vbsa_layout(bh, s, qn, kn);
@@ -992,7 +1029,7 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   int32_t* items = (int32_t*)(base + lay.items);
   int32_t* nitems = (int32_t*)(base + lay.nitems);
   int32_t* work = (int32_t*)(base + lay.work);
-  int32_t* order = (int32_t*)(base + lay.order);
+  int32_t* list = (int32_t*)(base + lay.list);
   constexpr int qtile = VbsaCfg<kDefaultQB>::kQTile;
   const size_t smem = (size_t)((EAR ? 4 : 2) * kn + 1) * sizeof(int32_t);
   // Half items need the kernel with a second set of K/V buffers (130 KB of static LDS with the row
@@ -1002,7 +1039,8 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   hipLaunchKernelGGL(vbsa_plan_kernel, dim3(bh), dim3(kPlanThreads), 0, st, q_sizes, k_sizes, map, EAR ? 1 : 0, work,
                      s, qn, kn, qtile, lay.cap, half_ok ? 1 : 0, qoff, koff, items, nitems, status);
   if (int rc = check_launch(name)) return rc;
-  hipLaunchKernelGGL(vbsa_order_kernel, dim3(1), dim3(kPlanThreads), 0, st, work, bh, order);
+  hipLaunchKernelGGL(vbsa_order_kernel, dim3(1), dim3(kPlanThreads), 0, st, work, nitems, bh, lay.cap,
+                     (s + qtile - 1) / qtile, list);
   if (int rc = check_launch(name)) return rc;
   const long long total_items = (long long)bh * lay.cap;
   const long long nblocks = (total_items + 8 * kXcdRun - 1) / (8 * kXcdRun) * (8 * kXcdRun);
@@ -1011,11 +1049,11 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   if (!EAR && half_ok)
     hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX, !EAR>), dim3((unsigned)nblocks), dim3(kVWaves * kWave),
                        smem, st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items,
-                       nitems, scale_log2, q_idx, k_idx, heads, order);
+                       nitems, scale_log2, q_idx, k_idx, heads, list);
   else
     hipLaunchKernelGGL((vbsa_attn_kernel<kDefaultQB, EAR, IDX, false>), dim3((unsigned)nblocks), dim3(kVWaves * kWave),
                        smem, st, q, k, v, kc, vc, map, k_sizes, o, s, qn, kn, lay.cap, total_items, qoff, koff, items,
-                       nitems, scale_log2, q_idx, k_idx, heads, order);
+                       nitems, scale_log2, q_idx, k_idx, heads, list);
   return check_launch(name);
 }
 }  // namespace
@@ -1039,7 +1077,7 @@ extern "C" int svoo_vbsa_fused_fwd(const uint16_t* q, const uint16_t* k, const u
 }
 
 // ------------------------------------------------------------------------------------------ allocation-free entry
-// svoo_vbsa_fused_fwd_noalloc keeps the plan (cluster offsets, work items, head order) in this file-scope
+// svoo_vbsa_fused_fwd_noalloc keeps the plan (cluster offsets, work items, work list) in this file-scope
 // device array instead of a caller workspace.  Each device holds its own copy; host code must use the
 // address hipGetSymbolAddress returns for the current device, never the array's name.
 static __device__ __align__(256) unsigned char scratch[SVOO_NOALLOC_SCRATCH_BYTES];

@@ -415,6 +415,47 @@ def test_vbsa_fills_heads_with_inconsistent_sizes_with_nan(gpu):
     assert torch.equal(fo[:, 0], out[0, 0])
 
 
+def _many_heads_case(bh, s, seed):
+    """bh heads of s tokens with 1 to 3 non-empty query clusters, random maps (so the heads' work and launch
+    ranks differ) and, on every 37th head, key sizes that do not sum to S."""
+    r = np.random.default_rng(seed)
+    patterns = np.array([[s, 0, 0], [s // 2, s - s // 2, 0], [1, 1, s - 2], [0, s, 0], [13, 14, s - 27]], np.int32)
+    qs = patterns[r.integers(0, len(patterns), bh)][None]
+    cut = r.integers(1, s, bh)
+    ks = np.stack([cut, s - cut], axis=1).astype(np.int32)[None]
+    bad = np.arange(bh) % 37 == 5
+    ks[0, bad, 1] -= 1
+    m = r.random((1, bh, 3, 2)) < 0.6
+    m[..., r.integers(0, 2)] = True
+    return qs, ks, m, bad
+
+
+@pytest.mark.parametrize("bh", [300, 4100])
+def test_vbsa_work_list_over_many_heads(gpu, bh):
+    """The work list the order kernel builds: heads ranked by work in chunks of 256 (bh = 300), or in their
+    own order past 4096 heads (bh = 4100), each contributing its items, or NaN-filling slots when its sizes
+    do not sum to S, with no slot lost or repeated."""
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd
+
+    s = 40
+    say("vbsa work list over", bh, "heads")
+    qs, ks, m, bad = _many_heads_case(bh, s, 60 + bh)
+    q, qt = rand_bf16((1, bh, s, 128), 61, gpu)
+    k, kt = rand_bf16((1, bh, s, 128), 62, gpu)
+    v, vt = rand_bf16((1, bh, s, 128), 63, gpu)
+    mt, qst, kst = torch.from_numpy(m).to(gpu), torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu)
+    out = dynamic_block_sparse_fwd(qt, kt, vt, mt, qst, kst, validate=False)
+    torch.cuda.synchronize()
+    o = out[0]
+    assert torch.isnan(o[torch.from_numpy(bad).to(gpu)]).all()
+    good = ~bad
+    assert not torch.isnan(o[torch.from_numpy(good).to(gpu)]).any()
+    # the oracle on every good head at bh = 300, on every 13th of 4100
+    pick = good & (np.arange(bh) % (1 if bh < 1000 else 13) == 0)
+    ref = O.block_sparse_attention(q[:, pick], k[:, pick], v[:, pick], m[:, pick], qs[:, pick], ks[:, pick])
+    _attn_check(out[:, torch.from_numpy(pick).to(gpu)], ref)
+
+
 def test_vbsa_segments_expand_to_reference_plan(gpu):
     from svoo_amd.co_clustering import vbsa_segments
 
