@@ -33,7 +33,8 @@ namespace svoo {
 
 constexpr int kVWaves = 8;
 constexpr int kKT = 64;          // keys per tile
-constexpr int kPlanThreads = 256;
+constexpr int kPlanThreads = 1024;  // plan kernel
+constexpr int kOrderThreads = 256;  // order kernel
 constexpr int kMaxKN = 4096;
 
 template <int QB>
@@ -117,25 +118,53 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
       if (!ok && status) atomicOr(status, 1);
     }
   }
-  // Work of the head in KV tiles (the attention's launch order runs heavy heads first): one wave per
-  // query cluster sums the stream length of its map row (active keys, plus the inactive centroids for
-  // EAR) and weighs it by the cluster's query tiles.
+  // Work of the head in KV tiles (the attention's launch order runs heavy heads first): a wave sums the
+  // stream length of a query cluster's map row (active keys, plus the inactive centroids for EAR) and
+  // weighs it by the cluster's query tiles.  The pass is bound by load latency, not bytes: a wave keeps
+  // four rows (i + r * kPW) in flight and reads a row 4 bytes per lane and load when its rows start 4-byte
+  // aligned, with the key sizes from LDS.
   {
+    __shared__ __attribute__((aligned(16))) int32_t s_ks[kMaxKN];
+    for (int j = tid; j < kn; j += kPlanThreads) s_ks[j] = ksb[j];
+    __syncthreads();
+    constexpr int kPW = kPlanThreads / kWave;
     const int wave = tid / kWave, lane = tid % kWave;
+    const bool words = kn % 4 == 0 && (uintptr_t)map % 4 == 0;
     long long wsum = 0;
-    for (int i = wave; i < qn; i += kPlanThreads / kWave) {
-      const uint8_t* mrow = map + ((size_t)b * qn + i) * kn;
-      int act = 0;
-      // both loads unconditional and 16 iterations unrolled: the loads of a row are in flight together
-#pragma unroll 16
-      for (int j = lane; j < kn; j += kWave) {
-        const int kv = ksb[j], on = mrow[j];
-        act += on ? kv : ear;
+    for (int i = wave; i < qn; i += 4 * kPW) {
+      int act[4] = {0, 0, 0, 0};
+      const uint8_t* mr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mr[r] = map + ((size_t)b * qn + min(i + r * kPW, qn - 1)) * kn;
+      if (words) {
+#pragma unroll 4
+        for (int w = lane; w < kn / 4; w += kWave) {
+          uint32_t m4[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) m4[r] = ((const uint32_t*)mr[r])[w];
+          const int4 k4 = *(const int4*)&s_ks[4 * w];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            act[r] += ((m4[r] & 0xffu) ? k4.x : ear) + ((m4[r] & 0xff00u) ? k4.y : ear) +
+                      ((m4[r] & 0xff0000u) ? k4.z : ear) + ((m4[r] >> 24) ? k4.w : ear);
+        }
+      } else {
+#pragma unroll 8
+        for (int j = lane; j < kn; j += kWave) {
+          const int kv = s_ks[j];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) act[r] += mr[r][j] ? kv : ear;
+        }
       }
 #pragma unroll
-      for (int o = kWave / 2; o > 0; o >>= 1) act += __shfl_xor(act, o);
-      const int v = qsb[i];
-      if (v > 0) wsum += (long long)((v + qtile - 1) / qtile) * (1 + (act + kKT - 1) / kKT);
+      for (int r = 0; r < 4; ++r) {
+        int a = act[r];
+#pragma unroll
+        for (int o = kWave / 2; o > 0; o >>= 1) a += __shfl_xor(a, o);
+        const int row = i + r * kPW;
+        const int v = row < qn ? qsb[row] : 0;
+        if (v > 0) wsum += (long long)((v + qtile - 1) / qtile) * (1 + (a + kKT - 1) / kKT);
+      }
     }
     __syncthreads();  // the scans above are done with red
     if (lane == 0) red[wave] = wsum;
@@ -155,29 +184,29 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
 // bh * cap entries.  A dense list gives every XCD an equal share of the real items: with per-head slot ranges
 // the unused slots at the end of each head's range fall on the same XCDs head after head.
 constexpr int kOrderMax = 4096;
-__global__ void __launch_bounds__(kPlanThreads) vbsa_order_kernel(const int32_t* __restrict__ work,
+__global__ void __launch_bounds__(kOrderThreads) vbsa_order_kernel(const int32_t* __restrict__ work,
                                                                   const int32_t* __restrict__ nitems, int bh, int cap,
                                                                   int nan_slots, int32_t* __restrict__ list) {
   __shared__ int32_t w[kOrderMax], rk[kOrderMax];  // work and rank of each head, then the head of each rank
-  __shared__ long long red[kPlanThreads / kWave];
-  __shared__ int32_t c_head[kPlanThreads], c_n[kPlanThreads], c_base[kPlanThreads];
+  __shared__ long long red[kOrderThreads / kWave];
+  __shared__ int32_t c_head[kOrderThreads], c_n[kOrderThreads], c_base[kOrderThreads];
   const int tid = threadIdx.x;
   const bool ranked = bh <= kOrderMax;
   if (ranked) {
-    for (int h = tid; h < bh; h += kPlanThreads) w[h] = work[h];
+    for (int h = tid; h < bh; h += kOrderThreads) w[h] = work[h];
     __syncthreads();
-    for (int h = tid; h < bh; h += kPlanThreads) {
+    for (int h = tid; h < bh; h += kOrderThreads) {
       const int wh = w[h];
       int rank = 0;
       for (int g = 0; g < bh; ++g) rank += (w[g] > wh || (w[g] == wh && g < h)) ? 1 : 0;
       rk[h] = rank;
     }
     __syncthreads();  // every thread is done reading the work values
-    for (int h = tid; h < bh; h += kPlanThreads) w[rk[h]] = h;
+    for (int h = tid; h < bh; h += kOrderThreads) w[rk[h]] = h;
     __syncthreads();
   }
   long long run = 0;
-  for (int r0 = 0; r0 < bh; r0 += kPlanThreads) {
+  for (int r0 = 0; r0 < bh; r0 += kOrderThreads) {
     const int r = r0 + tid;
     int n = 0, h = 0;
     if (r < bh) {
@@ -186,20 +215,20 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_order_kernel(const int32_t*
       n = ni >= 0 ? ni : nan_slots;
     }
     long long tot;
-    const long long ex = block_exclusive_scan_i64<kPlanThreads>(n, red, &tot);
+    const long long ex = block_exclusive_scan_i64<kOrderThreads>(n, red, &tot);
     c_head[tid] = h;
     c_n[tid] = n;
     c_base[tid] = (int32_t)(run + ex);
     __syncthreads();
-    const int m = min(kPlanThreads, bh - r0);
+    const int m = min(kOrderThreads, bh - r0);
     for (int i = 0; i < m; ++i) {
       const int32_t tag = c_head[i] << 15, base = c_base[i];
-      for (int j = tid; j < c_n[i]; j += kPlanThreads) list[base + j] = tag | j;
+      for (int j = tid; j < c_n[i]; j += kOrderThreads) list[base + j] = tag | j;
     }
     __syncthreads();  // the chunk's tables are read before the next chunk writes them
     run += tot;
   }
-  for (long long i = run + tid; i < (long long)bh * cap; i += kPlanThreads) list[i] = -1;
+  for (long long i = run + tid; i < (long long)bh * cap; i += kOrderThreads) list[i] = -1;
 }
 
 // Compacts the active key clusters of one map row into (start, cumulative length) segments in
@@ -1039,7 +1068,7 @@ int vbsa_launch(const char* name, const uint16_t* q, const uint16_t* k, const ui
   hipLaunchKernelGGL(vbsa_plan_kernel, dim3(bh), dim3(kPlanThreads), 0, st, q_sizes, k_sizes, map, EAR ? 1 : 0, work,
                      s, qn, kn, qtile, lay.cap, half_ok ? 1 : 0, qoff, koff, items, nitems, status);
   if (int rc = check_launch(name)) return rc;
-  hipLaunchKernelGGL(vbsa_order_kernel, dim3(1), dim3(kPlanThreads), 0, st, work, nitems, bh, lay.cap,
+  hipLaunchKernelGGL(vbsa_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, work, nitems, bh, lay.cap,
                      (s + qtile - 1) / qtile, list);
   if (int rc = check_launch(name)) return rc;
   const long long total_items = (long long)bh * lay.cap;
