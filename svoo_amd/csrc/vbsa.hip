@@ -2,7 +2,8 @@
 //
 // Plan (one block per batch-head, on device, no host round trip):
 //   qoff/koff = exclusive prefix of the cluster sizes (validated to sum to S), and a work list of
-//   (q-cluster, q-tile) items, kQTile queries each.
+//   (q-cluster, q-tile) items, kQTile queries each, the query clusters with the longest KV streams first.
+// Order (one block): heads by estimated work, heaviest first, and the grid's work list, head after head.
 // Attention (one block of 8 waves per work item of 256 queries, 32 queries per wave):
 //   * the block compacts its map row into a list of active key segments (start, length) in LDS;
 //     the KV stream is their concatenation (ascending cluster), cut into 64-key tiles that span
@@ -35,6 +36,8 @@ constexpr int kVWaves = 8;
 constexpr int kKT = 64;          // keys per tile
 constexpr int kPlanThreads = 1024;  // plan kernel
 constexpr int kOrderThreads = 256;  // order kernel
+constexpr int kPlanSortMax = 4096;  // heads with at most this many query clusters get their items longest first
+constexpr int kPlanBuckets = 4096;
 constexpr int kMaxKN = 4096;
 
 template <int QB>
@@ -84,6 +87,7 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
     }
   }
   // qoff and the tile counts (packed: tiles << 32 | rows)
+  bool ok;
   {
     const int per = (qn + kPlanThreads - 1) / kPlanThreads;
     const int i0 = min(qn, tid * per), i1 = min(qn, i0 + per);
@@ -97,7 +101,7 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
     long long tot;
     long long run = block_exclusive_scan_i64<kPlanThreads>(loc, red, &tot);
     __syncthreads();
-    const bool ok = !bad && (int)(tot & 0xffffffffll) == s && (int)(tot >> 32) <= cap;
+    ok = !bad && (int)(tot & 0xffffffffll) == s && (int)(tot >> 32) <= cap;
     for (int i = i0; i < i1; ++i) {
       const int v = qsb[i];
       qo[i] = (int32_t)(run & 0xffffffffll);
@@ -107,7 +111,7 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
       // the LDS for a second KV stream
       const int rem = v - (nt - 1) * qtile;
       const int hflag = (half_ok && 2 * rem <= qtile) ? 0x8000 : 0;
-      if (ok)
+      if (ok && qn > kPlanSortMax)
         for (int t = 0; t < nt; ++t) items[(size_t)b * cap + t0 + t] = (i << 16) | t | (t == nt - 1 ? hflag : 0);
       run += ((long long)nt << 32) | (long long)(uint32_t)v;
     }
@@ -125,6 +129,7 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
   // aligned, with the key sizes from LDS.
   {
     __shared__ __attribute__((aligned(16))) int32_t s_ks[kMaxKN];
+    __shared__ int32_t s_tiles[kPlanSortMax];  // KV tiles of each query cluster's stream
     for (int j = tid; j < kn; j += kPlanThreads) s_ks[j] = ksb[j];
     __syncthreads();
     constexpr int kPW = kPlanThreads / kWave;
@@ -164,6 +169,7 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
         const int row = i + r * kPW;
         const int v = row < qn ? qsb[row] : 0;
         if (v > 0) wsum += (long long)((v + qtile - 1) / qtile) * (1 + (a + kKT - 1) / kKT);
+        if (lane == 0 && row < qn && qn <= kPlanSortMax) s_tiles[row] = (a + kKT - 1) / kKT;
       }
     }
     __syncthreads();  // the scans above are done with red
@@ -173,6 +179,49 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
       long long w = 0;
       for (int i = 0; i < kPlanThreads / kWave; ++i) w += red[i];
       work[b] = (int32_t)min(w, 0x7fffffffll);
+    }
+    // The head's work items, longest first: query clusters by the length of their KV stream in tiles (0.72 of it
+    // for a cluster that is one half item), the items of a cluster together (they read the same keys).  A
+    // counting sort over kPlanBuckets lengths (longer ones share the last bucket); the order of equal lengths
+    // is free.  Heads with more than kPlanSortMax clusters keep the cluster order (written above).
+    if (ok && qn <= kPlanSortMax) {
+      __shared__ int32_t s_bk[kPlanBuckets];
+      auto bucket = [&](int i, int v) {
+        const int nt = (v + qtile - 1) / qtile, rem = v - (nt - 1) * qtile;
+        const int tl = (nt == 1 && half_ok && 2 * rem <= qtile) ? (s_tiles[i] * 23) / 32 : s_tiles[i];
+        return kPlanBuckets - 1 - min(tl, kPlanBuckets - 1);
+      };
+      for (int e = tid; e < kPlanBuckets; e += kPlanThreads) s_bk[e] = 0;
+      __syncthreads();
+      for (int i = tid; i < qn; i += kPlanThreads) {
+        const int v = qsb[i];
+        if (v > 0) atomicAdd(&s_bk[bucket(i, v)], (v + qtile - 1) / qtile);
+      }
+      __syncthreads();
+      constexpr int kPer = kPlanBuckets / kPlanThreads;
+      int c[kPer];
+      long long loc = 0;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        c[e] = s_bk[tid * kPer + e];
+        loc += c[e];
+      }
+      long long tot;
+      long long run = block_exclusive_scan_i64<kPlanThreads>(loc, red, &tot);  // its barriers follow the reads
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        s_bk[tid * kPer + e] = (int32_t)run;
+        run += c[e];
+      }
+      __syncthreads();
+      for (int i = tid; i < qn; i += kPlanThreads) {
+        const int v = qsb[i];
+        if (v <= 0) continue;
+        const int nt = (v + qtile - 1) / qtile, rem = v - (nt - 1) * qtile;
+        const int hflag = (half_ok && 2 * rem <= qtile) ? 0x8000 : 0;
+        const int pos = atomicAdd(&s_bk[bucket(i, v)], nt);
+        for (int t = 0; t < nt; ++t) items[(size_t)b * cap + pos + t] = (i << 16) | t | (t == nt - 1 ? hflag : 0);
+      }
     }
   }
 }

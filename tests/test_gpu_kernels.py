@@ -456,6 +456,29 @@ def test_vbsa_work_list_over_many_heads(gpu, bh):
     _attn_check(out[:, torch.from_numpy(pick).to(gpu)], ref)
 
 
+def test_vbsa_many_query_clusters_keep_cluster_order(gpu):
+    """A head with more than 4096 query clusters is planned in cluster order (the longest-first sort covers
+    up to 4096): one head of 5000 clusters of 1-3 queries, every item a half item, against the oracle."""
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd
+
+    say("vbsa 5000 query clusters")
+    r = np.random.default_rng(81)
+    qn, kn = 5000, 24
+    qsz = r.integers(1, 4, qn).astype(np.int32)
+    s = int(qsz.sum())
+    cuts = np.sort(r.choice(np.arange(1, s), size=kn - 1, replace=False))
+    ks = np.diff(np.concatenate([[0], cuts, [s]])).astype(np.int32)[None, None]
+    qs = qsz[None, None]
+    m = r.random((1, 1, qn, kn)) < 0.3
+    m[..., 0] = True
+    q, qt = rand_bf16((1, 1, s, 128), 82, gpu)
+    k, kt = rand_bf16((1, 1, s, 128), 83, gpu)
+    v, vt = rand_bf16((1, 1, s, 128), 84, gpu)
+    mt, qst, kst = torch.from_numpy(m).to(gpu), torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu)
+    out = dynamic_block_sparse_fwd(qt, kt, vt, mt, qst, kst)
+    _attn_check(out, O.block_sparse_attention(q, k, v, m, qs, ks))
+
+
 def test_vbsa_segments_expand_to_reference_plan(gpu):
     from svoo_amd.co_clustering import vbsa_segments
 
