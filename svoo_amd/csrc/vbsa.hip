@@ -180,22 +180,23 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
       for (int i = 0; i < kPlanThreads / kWave; ++i) w += red[i];
       work[b] = (int32_t)min(w, 0x7fffffffll);
     }
-    // The head's work items, longest first: query clusters by the length of their KV stream in tiles (0.72 of it
-    // for a cluster that is one half item), the items of a cluster together (they read the same keys).  A
-    // counting sort over kPlanBuckets lengths (longer ones share the last bucket); the order of equal lengths
-    // is free.  Heads with more than kPlanSortMax clusters keep the cluster order (written above).
+    // The head's work items, longest first: an item's length is its cluster's KV stream in tiles, 0.72 of it for
+    // a half item; a cluster's full items stay together (they read the same keys), its half item goes with the
+    // other half items of its length.  A counting sort over kPlanBuckets lengths (longer ones share the last
+    // bucket); the order of equal lengths is free.  Heads with more than kPlanSortMax clusters keep the cluster
+    // order (written above).
     if (ok && qn <= kPlanSortMax) {
       __shared__ int32_t s_bk[kPlanBuckets];
-      auto bucket = [&](int i, int v) {
-        const int nt = (v + qtile - 1) / qtile, rem = v - (nt - 1) * qtile;
-        const int tl = (nt == 1 && half_ok && 2 * rem <= qtile) ? (s_tiles[i] * 23) / 32 : s_tiles[i];
-        return kPlanBuckets - 1 - min(tl, kPlanBuckets - 1);
-      };
+      auto bk = [&](int tl) { return kPlanBuckets - 1 - min(tl, kPlanBuckets - 1); };
       for (int e = tid; e < kPlanBuckets; e += kPlanThreads) s_bk[e] = 0;
       __syncthreads();
       for (int i = tid; i < qn; i += kPlanThreads) {
         const int v = qsb[i];
-        if (v > 0) atomicAdd(&s_bk[bucket(i, v)], (v + qtile - 1) / qtile);
+        if (v <= 0) continue;
+        const int nt = (v + qtile - 1) / qtile, rem = v - (nt - 1) * qtile;
+        const bool hl = half_ok && 2 * rem <= qtile;
+        if (nt - (hl ? 1 : 0) > 0) atomicAdd(&s_bk[bk(s_tiles[i])], nt - (hl ? 1 : 0));
+        if (hl) atomicAdd(&s_bk[bk((s_tiles[i] * 23) / 32)], 1);
       }
       __syncthreads();
       constexpr int kPer = kPlanBuckets / kPlanThreads;
@@ -218,9 +219,13 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
         const int v = qsb[i];
         if (v <= 0) continue;
         const int nt = (v + qtile - 1) / qtile, rem = v - (nt - 1) * qtile;
-        const int hflag = (half_ok && 2 * rem <= qtile) ? 0x8000 : 0;
-        const int pos = atomicAdd(&s_bk[bucket(i, v)], nt);
-        for (int t = 0; t < nt; ++t) items[(size_t)b * cap + pos + t] = (i << 16) | t | (t == nt - 1 ? hflag : 0);
+        const bool hl = half_ok && 2 * rem <= qtile;
+        const int nf = nt - (hl ? 1 : 0);
+        if (nf > 0) {
+          const int pos = atomicAdd(&s_bk[bk(s_tiles[i])], nf);
+          for (int t = 0; t < nf; ++t) items[(size_t)b * cap + pos + t] = (i << 16) | t;
+        }
+        if (hl) items[(size_t)b * cap + atomicAdd(&s_bk[bk((s_tiles[i] * 23) / 32)], 1)] = (i << 16) | (nt - 1) | 0x8000;
       }
     }
   }
