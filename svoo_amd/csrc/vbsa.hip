@@ -27,6 +27,7 @@
 // (key, value) centroids of the inactive clusters, each scored q . kc_j / sqrt(D) + log(|K_j| + 1e-6),
 // so one online softmax covers both (the reference's token attention + log-sum-exp merge).
 #include <mutex>
+#include <type_traits>
 
 #include "svoo_common.h"
 
@@ -110,9 +111,11 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
       // a last tile of at most qtile / 2 queries is a half item (flag 0x8000) when the kernel has
       // the LDS for a second KV stream
       const int rem = v - (nt - 1) * qtile;
-      const int hflag = (half_ok && 2 * rem <= qtile) ? 0x8000 : 0;
+      // last tile: a half item (0x8000) up to qtile / 2 queries, B-chunked (bit 31) up to 3 qtile / 4
+      const uint32_t hflag = !half_ok ? 0u : 2 * rem <= qtile ? 0x8000u : 4 * rem <= 3 * qtile ? 0x80000000u : 0u;
       if (ok && qn > kPlanSortMax)
-        for (int t = 0; t < nt; ++t) items[(size_t)b * cap + t0 + t] = (i << 16) | t | (t == nt - 1 ? hflag : 0);
+        for (int t = 0; t < nt; ++t)
+          items[(size_t)b * cap + t0 + t] = (int32_t)(((uint32_t)i << 16) | (uint32_t)t | (t == nt - 1 ? hflag : 0u));
       run += ((long long)nt << 32) | (long long)(uint32_t)v;
     }
     if (tid == 0) {
@@ -223,7 +226,9 @@ __global__ void __launch_bounds__(kPlanThreads) vbsa_plan_kernel(const int32_t* 
         const int nf = nt - (hl ? 1 : 0);
         if (nf > 0) {
           const int pos = atomicAdd(&s_bk[bk(s_tiles[i])], nf);
-          for (int t = 0; t < nf; ++t) items[(size_t)b * cap + pos + t] = (i << 16) | t;
+          const uint32_t bflag = (half_ok && 4 * rem <= 3 * qtile) ? 0x80000000u : 0u;  // B-chunked last tile
+          for (int t = 0; t < nf; ++t)
+            items[(size_t)b * cap + pos + t] = (int32_t)(((uint32_t)i << 16) | (uint32_t)t | (t == nt - 1 ? bflag : 0u));
         }
         if (hl) items[(size_t)b * cap + atomicAdd(&s_bk[bk((s_tiles[i] * 23) / 32)], 1)] = (i << 16) | (nt - 1) | 0x8000;
       }
@@ -402,7 +407,12 @@ __device__ __forceinline__ int cursor_row(KvCursor& c, const int32_t* seg_start,
 // queries is taken by both groups, each wave of a group holding the same 32 queries as its partner
 // in the other group; group A walks the even tiles of the KV stream (stream 0), group B the odd
 // ones (stream 1), on the same half-step schedule, and the two online-softmax states are merged
-// through LDS at the end, so such an item costs about half the time of a full one.  Each group copies
+// through LDS at the end, so such an item costs about half the time of a full one.
+// B-chunked items (HC kernels: a last tile of 129 to 192 queries, so group B holds at most 64): group B's
+// waves wg and wg + 2 hold the same 32 queries and take the first and the second 32 keys of every tile (16
+// MFMAs and 16 exponentials per wave and tile), group B resolves the row tables (waves 4 and 5) in place of
+// waves 0 and 1, and the two states of a query merge through LDS at the end.
+// Half items: each group copies
 // its own stream's tiles during its softmax, and group A's waves resolve the four row tables (one
 // each) at the start of their MFMA half-step, where they would otherwise wait at the barrier for
 // group B's longer softmax with copies.
@@ -447,9 +457,10 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     }
     return;
   }
-  const int packed = items[(size_t)b * cap + local];
-  const int ci = packed >> 16, tile = packed & 0x7fff;
-  const bool half = HC && (packed & 0x8000) != 0;
+  const uint32_t packed = (uint32_t)items[(size_t)b * cap + local];
+  const int ci = (int)((packed >> 16) & 0x7fff), tile = (int)(packed & 0x7fff);
+  const bool half = HC && (packed & 0x8000u) != 0;
+  const bool bchunk = HC && (packed >> 31) != 0;  // a full item whose group B holds at most 64 queries
   const int32_t* qo = qoff + (size_t)b * (qn + 1);
   const int q0 = qo[ci] + tile * kQTile;
   const int q1 = min(qo[ci + 1], q0 + kQTile);
@@ -507,7 +518,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     return;
   }
   // full item: group A owns queries 0-127, group B 128-255; half item: both own queries 0-127
-  const int qrow0 = q0 + ((group_b && !half) ? 128 : 0) + wg * 32;
+  const int qrow0 = q0 + ((group_b && !half) ? 128 : 0) + ((bchunk && group_b) ? (wg & 1) : wg) * 32;
   const bool active = qrow0 < q1;
 
   u32x4_t qop[8];
@@ -529,7 +540,7 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
   int last_row = nseg > 0 ? seg_start[nseg - 1] + (total_tok - 1 - seg_cum[nseg - 1]) : 0;
   if constexpr (IDX) last_row = kix[last_row];
   KvCursor cursor;
-  const bool resolver = (half ? wave < 4 : wave < 2) && nseg > 0;
+  const bool resolver = (half ? wave < 4 : bchunk ? (wave == 4 || wave == 5) : wave < 2) && nseg > 0;
   const int p_first = (half && wave >= 2 ? kKT : 0) + lane;  // this lane's row in the wave's first tile
   if (resolver) cursor_init(cursor, seg_start, seg_cum, nseg, min(p_first, total_tok - 1));
   // IDX: the token index of this lane's row in the next tile the wave resolves, loaded one call
@@ -765,91 +776,289 @@ __global__ void __launch_bounds__(kVWaves * kWave) __attribute__((amdgpu_waves_p
     }
     l_run += lsum;
   };
+  // B-chunked items: group B's phases on the wave's 32-key chunk of a tile (its rows 32 rows further in
+  // every K and V buffer; the swizzle depends on the row mod 16, so the chunk's rows read as rows 0-31),
+  // with the scores and P of the chunk in sacc[0] and pop[0].
+  const int chunk = (bchunk && group_b) ? (wg >> 1) : 0;
+  if (chunk) {
+    // the chunk's rows start 32 rows into every K and V buffer: folded into the lane offsets once
+#pragma unroll
+    for (int ks2 = 0; ks2 < 8; ++ks2) koffs[ks2] += 32 * 128;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      voffs[0][db] += 32 * 128;
+      voffs[1][db] += 32 * 128;
+    }
+  }
+  auto scores_q = [&](const uint16_t* kt) __attribute__((always_inline)) {
+    sacc[0] = f32x16_t{};
+#pragma unroll
+    for (int ks2 = 0; ks2 < 8; ++ks2)
+      sacc[0] = mfma32x32x16(as_bf16x8(*(const u32x4_t*)(&kt[koffs[ks2]])), as_bf16x8(qop[ks2]), sacc[0]);
+  };
+  auto mop_q = [&](int i, const uint16_t* vt, const uint16_t* knext) __attribute__((always_inline)) -> u32x4_t {
+    if (i < 8) {
+      const int st = i / 4, db = i % 4;
+      const int rb = st * 16 * 128;
+      const uint2 lo = ds_read_tr16_b64(&vt[rb + voffs[0][db]]);
+      const uint2 hi = ds_read_tr16_b64(&vt[rb + voffs[1][db]]);
+      return u32x4_t{lo.x, lo.y, hi.x, hi.y};
+    }
+    return *(const u32x4_t*)(&knext[koffs[i - 8]]);
+  };
+  auto mphase_q = [&](const uint16_t* vt, const uint16_t* knext) __attribute__((always_inline)) {
+    u32x4_t buf[3];
+    buf[0] = mop_q(0, vt, knext);
+    buf[1] = mop_q(1, vt, knext);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    auto mm = [&](int i) __attribute__((always_inline)) {
+      if (i < 8) {
+        const int st = i / 4, db = i % 4;
+        acc[db] = mfma32x32x16(as_bf16x8(buf[i % 3]), as_bf16x8(pop[0][st]), acc[db]);
+      } else {
+        if (i == 8) sacc[0] = f32x16_t{};
+        sacc[0] = mfma32x32x16(as_bf16x8(buf[i % 3]), as_bf16x8(qop[i - 8]), sacc[0]);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      buf[(i + 2) % 3] = mop_q(i + 2, vt, knext);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      mm(i);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+#pragma unroll
+    for (int i = 6; i < 14; ++i) {
+      buf[(i + 2) % 3] = mop_q(i + 2, vt, knext);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      mm(i);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    mm(14);
+    mm(15);
+  };
+  // Softmax of the chunk of tile t; the eight copies of a copying wave go out one per two exponentials.
+  // Only called for a chunk that holds a key (so the running maximum is finite after the first call).
+  auto vphase_q = [&](int t, bool dmaon = false, int4 rk4 = int4{}, uint16_t* kdst = nullptr, int4 rv4 = int4{},
+                      uint16_t* vdst = nullptr) __attribute__((always_inline)) {
+    const int tbase = t * kKT + chunk * 32;
+    if (tbase + 32 > total) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = (r / 4) * 8 + h * 4 + (r % 4);
+        if (tbase + key >= total) sacc[0][r] = -INFINITY;
+      }
+    }
+    auto pexp = [&](bool dm) __attribute__((always_inline)) -> float {
+      const float mneg = -m_run;
+      const int rka[4] = {rk4.x, rk4.y, rk4.z, rk4.w}, rva[4] = {rv4.x, rv4.y, rv4.z, rv4.w};
+      float la[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float pv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        pv[r] = __builtin_amdgcn_exp2f(fmaf(sacc[0][r], scale_log2, mneg));
+        if (dm && r % 2 == 1) {
+          const int j = r / 2;
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+          if (j < kDmaIt)
+            dma_one(kb, rka[j], j, kdst);
+          else
+            dma_one(vb, rva[j - kDmaIt], j - kDmaIt, vdst);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+      }
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pop[0][st][e] = cvt_pk_bf16(pv[8 * st + 2 * e], pv[8 * st + 2 * e + 1]);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) la[r % 4] += pv[r];
+      return (la[0] + la[1]) + (la[2] + la[3]);
+    };
+    float lsum = dmaon ? pexp(true) : pexp(false);
+    if (__any(!(lsum <= 8192.0f))) {
+      float mx = sacc[0][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sacc[0][r]);
+      mx = xhalf_max(mx) * scale_log2;
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+      lsum = pexp(false);
+    }
+    l_run += lsum;
+  };
   if (!half) {
-    // Prologue: tables K(0), K(1), V(0), V(1) (a table past the stream holds the last row, so copies
-    // of tiles past the end stay inside this head); DMA K(0), V(0) -> buffers 0, K(1) -> K buffer 1;
-    // S(0) everywhere, V(0) in group A; tables K(2), K(3), V(2); group B reads the rows of its first
-    // copies (K(2), V(1)).
-    if (wave == 0) {
-      resolve(rowtab[0][0][0], 0, 1);
-      resolve(rowtab[0][0][1], 1, 1);
-    }
-    if (wave == 1) {
-      resolve(rowtab[0][1][0], 0, 1);
-      resolve(rowtab[0][1][1], 1, 1);
-    }
-    __syncthreads();
-    if (group_b) {
-      dma(kb, rowtab[0][0][0], k_s0);
-      dma(vb, rowtab[0][1][0], v_s0);
-      if (ntiles > 1) dma(kb, rowtab[0][0][1], k_s1);
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    __syncthreads();
-    if (active) scores(k_s0);
-    if (active && !group_b) vphase(0);
-    if (wave == 0) {
-      resolve(rowtab[0][0][0], 2, 1);
-      resolve(rowtab[0][0][1], 3, 1);
-    }
-    if (wave == 1) resolve(rowtab[0][1][0], 2, 1);
-    __syncthreads();
-    int4 rk = make_int4(0, 0, 0, 0), rv = make_int4(0, 0, 0, 0);
-    if (group_b) {
-      rk = dma_rows(rowtab[0][0][0]);
-      rv = dma_rows(rowtab[0][1][1]);
-    }
+    // B-chunked items (kB): group B's waves wg and wg + 2 hold the same 32 queries and take the two 32-key
+    // halves of every tile (its phases half as long), and group B resolves the row tables (waves 4 and 5, after
+    // its MFMA phase) in place of waves 0 and 1.  The loop in two copies, one per item kind.
+    const int nt1 = total > 32 ? (total - 32 + kKT - 1) / kKT : 0;  // tiles with a key in their second half
+    const int nvb = __builtin_amdgcn_readfirstlane(chunk == 1 ? nt1 : ntiles);  // tiles of a B wave's chunk
+    auto full_loop = [&](auto bchunk_tag) __attribute__((always_inline)) -> bool {
+      constexpr bool kB = decltype(bchunk_tag)::value;
+      constexpr int rw0 = kB ? 4 : 0, rw1 = kB ? 5 : 1;  // the resolving waves
+      auto bvph = [&](int t, int4 rk4, uint16_t* kdst, int4 rv4, uint16_t* vdst) __attribute__((always_inline)) {
+        if constexpr (kB)
+          vphase_q(t, true, rk4, kdst, rv4, vdst);
+        else
+          vphase(t, true, rk4, kdst, rv4, vdst);
+      };
+      auto bmph = [&](const uint16_t* vt, const uint16_t* knext) __attribute__((always_inline)) {
+        if constexpr (kB)
+          mphase_q(vt, knext);
+        else
+          mphase(0, vt, knext);
+      };
+      // Prologue: tables K(0), K(1), V(0), V(1) (a table past the stream holds the last row, so copies
+      // of tiles past the end stay inside this head); DMA K(0), V(0) -> buffers 0, K(1) -> K buffer 1;
+      // S(0) everywhere, V(0) in group A; tables K(2), K(3), V(2); group B reads the rows of its first
+      // copies (K(2), V(1)).
+      if (wave == rw0) {
+        resolve(rowtab[0][0][0], 0, 1);
+        resolve(rowtab[0][0][1], 1, 1);
+      }
+      if (wave == rw1) {
+        resolve(rowtab[0][1][0], 0, 1);
+        resolve(rowtab[0][1][1], 1, 1);
+      }
+      __syncthreads();
+      if (group_b) {
+        dma(kb, rowtab[0][0][0], k_s0);
+        dma(vb, rowtab[0][1][0], v_s0);
+        if (ntiles > 1) dma(kb, rowtab[0][0][1], k_s1);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __syncthreads();
+      if constexpr (kB) {
+        if (!group_b) {
+          if (active) {
+            scores(k_s0);
+            vphase(0);
+          }
+        } else if (active && nvb > 0) {
+          scores_q(k_s0);
+        }
+      } else {
+        if (active) scores(k_s0);
+        if (active && !group_b) vphase(0);
+      }
+      if (wave == rw0) {
+        resolve(rowtab[0][0][0], 2, 1);
+        resolve(rowtab[0][0][1], 3, 1);
+      }
+      if (wave == rw1) resolve(rowtab[0][1][0], 2, 1);
+      __syncthreads();
+      int4 rk = make_int4(0, 0, 0, 0), rv = make_int4(0, 0, 0, 0);
+      if (group_b) {
+        rk = dma_rows(rowtab[0][0][0]);
+        rv = dma_rows(rowtab[0][1][1]);
+      }
 
-    // Half-steps h = 0 .. 2T-1 (unrolled by 4: tile parity fixes the buffers).
-    //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1), tables K(t+4) and V(t+3) (waves 0, 1)
-    //   B: h = 2t -> V(t) with the copies of K(t+2) and V(t+1) spread through it;
-    //      h = 2t+1 -> M(t), rows of the next copies K(t+3) and V(t+2), wait for the copies.
-    // Copies run for tiles past the end too (rows from the tables), so the phases carry no branches.
-    for (int t = 0; t < ntiles; t += 2) {
-      // tile t (even): V(t) in v_s0, K(t+1) in k_s1
-      if (!group_b) {
-        if (active) mphase(t, v_s0, k_s1);
-      } else {
-        if (active)
-          vphase(t, true, rk, k_s0, rv, v_s1);
-        else
-          dma_all(rk, k_s0, rv, v_s1);
+      // Half-steps h = 0 .. 2T-1 (unrolled by 4: tile parity fixes the buffers).
+      //   A: h = 2t -> M(t);  h = 2t+1 -> V(t+1), tables K(t+4) and V(t+3) (waves 0, 1)
+      //   B: h = 2t -> V(t) with the copies of K(t+2) and V(t+1) spread through it;
+      //      h = 2t+1 -> M(t), rows of the next copies K(t+3) and V(t+2), wait for the copies.
+      // Copies run for tiles past the end too (rows from the tables), so the phases carry no branches.
+      for (int t = 0; t < ntiles; t += 2) {
+        // tile t (even): V(t) in v_s0, K(t+1) in k_s1
+        if (!group_b) {
+          if (active) mphase(t, v_s0, k_s1);
+        } else {
+          if (active && (!kB || t < nvb))
+            bvph(t, rk, k_s0, rv, v_s1);
+          else
+            dma_all(rk, k_s0, rv, v_s1);
+        }
+        __syncthreads();
+        if (!group_b) {
+          if (active && t + 1 < ntiles) vphase(t + 1);
+          if constexpr (!kB) {
+            if (wave == 0 && t + 4 < ntiles) resolve(rowtab[0][0][t & 1], t + 4, 1);
+            if (wave == 1 && t + 3 < ntiles) resolve(rowtab[0][1][(t + 1) & 1], t + 3, 1);
+          }
+        } else {
+          if (active && (!kB || t < nvb)) bmph(v_s0, k_s1);
+          if constexpr (kB) {
+            if (wave == 4 && t + 4 < ntiles) resolve(rowtab[0][0][t & 1], t + 4, 1);
+            if (wave == 5 && t + 3 < ntiles) resolve(rowtab[0][1][(t + 1) & 1], t + 3, 1);
+          }
+          rk = dma_rows(rowtab[0][0][(t + 1) & 1]);
+          rv = dma_rows(rowtab[0][1][t & 1]);
+          __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
+        if (t + 1 >= ntiles) break;
+        // tile t+1 (odd): V(t+1) in v_s1, K(t+2) in k_s0
+        if (!group_b) {
+          if (active) mphase(t + 1, v_s1, k_s0);
+        } else {
+          if (active && (!kB || t + 1 < nvb))
+            bvph(t + 1, rk, k_s1, rv, v_s0);
+          else
+            dma_all(rk, k_s1, rv, v_s0);
+        }
+        __syncthreads();
+        if (!group_b) {
+          if (active && t + 2 < ntiles) vphase(t + 2);
+          if constexpr (!kB) {
+            if (wave == 0 && t + 5 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 5, 1);
+            if (wave == 1 && t + 4 < ntiles) resolve(rowtab[0][1][t & 1], t + 4, 1);
+          }
+        } else {
+          if (active && (!kB || t + 1 < nvb)) bmph(v_s1, k_s0);
+          if constexpr (kB) {
+            if (wave == 4 && t + 5 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 5, 1);
+            if (wave == 5 && t + 4 < ntiles) resolve(rowtab[0][1][t & 1], t + 4, 1);
+          }
+          rk = dma_rows(rowtab[0][0][t & 1]);
+          rv = dma_rows(rowtab[0][1][(t + 1) & 1]);
+          __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();
       }
-      __syncthreads();
-      if (!group_b) {
-        if (active && t + 1 < ntiles) vphase(t + 1);
-        if (wave == 0 && t + 4 < ntiles) resolve(rowtab[0][0][t & 1], t + 4, 1);
-        if (wave == 1 && t + 3 < ntiles) resolve(rowtab[0][1][(t + 1) & 1], t + 3, 1);
-      } else {
-        if (active) mphase(t, v_s0, k_s1);
-        rk = dma_rows(rowtab[0][0][(t + 1) & 1]);
-        rv = dma_rows(rowtab[0][1][t & 1]);
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+      // B-chunked: the chunk-1 waves' states (queries 128 + 32 (wg & 1) ..) merge into the chunk-0 waves'
+      // (every wave takes part in the barriers; the K/V buffers are free after the loop's last barrier)
+      if constexpr (kB) {
+        float* ob_lds[4] = {(float*)k_s0, (float*)k_s1, (float*)v_s0, (float*)v_s1};
+        float2* ml_lds = (float2*)k1_s0;
+        const int sl = (wg & 1) * kWave + lane;
+        if (group_b && active && chunk == 1) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+              ((f32x4_t*)ob_lds[db])[r4 * 256 + sl] =
+                  f32x4_t{acc[db][4 * r4], acc[db][4 * r4 + 1], acc[db][4 * r4 + 2], acc[db][4 * r4 + 3]};
+          ml_lds[sl] = make_float2(m_run, l_run);
+        }
+        __syncthreads();
+        if (group_b && active && chunk == 0) {
+          const float2 mlb = ml_lds[sl];
+          const float m = fmaxf(m_run, mlb.x);
+          // chunk 0 holds tile 0's first key, so m is finite; an empty chunk 1 has m = -inf and weight 0
+          const float wa = __builtin_amdgcn_exp2f(m_run - m), wb = __builtin_amdgcn_exp2f(mlb.x - m);
+          l_run = l_run * wa + mlb.y * wb;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+              const f32x4_t o2 = ((const f32x4_t*)ob_lds[db])[r4 * 256 + sl];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[db][4 * r4 + e] = acc[db][4 * r4 + e] * wa + o2[e] * wb;
+            }
+        }
+        return !(group_b && chunk == 1);
       }
-      __syncthreads();
-      if (t + 1 >= ntiles) break;
-      // tile t+1 (odd): V(t+1) in v_s1, K(t+2) in k_s0
-      if (!group_b) {
-        if (active) mphase(t + 1, v_s1, k_s0);
-      } else {
-        if (active)
-          vphase(t + 1, true, rk, k_s1, rv, v_s0);
-        else
-          dma_all(rk, k_s1, rv, v_s0);
-      }
-      __syncthreads();
-      if (!group_b) {
-        if (active && t + 2 < ntiles) vphase(t + 2);
-        if (wave == 0 && t + 5 < ntiles) resolve(rowtab[0][0][(t + 1) & 1], t + 5, 1);
-        if (wave == 1 && t + 4 < ntiles) resolve(rowtab[0][1][t & 1], t + 4, 1);
-      } else {
-        if (active) mphase(t + 1, v_s1, k_s0);
-        rk = dma_rows(rowtab[0][0][t & 1]);
-        rv = dma_rows(rowtab[0][1][(t + 1) & 1]);
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      }
-      __syncthreads();
-    }
+      return true;
+    };
+    const bool keep = bchunk ? full_loop(std::true_type{}) : full_loop(std::false_type{});
+    if (!keep) return;
   } else if constexpr (HC) {
     // Half item: local tile u of stream x is global tile 2u + x; stream 0 (n0 tiles) lives in the
     // k_s / v_s buffers and is used by group A, stream 1 (n1 tiles) in k1_s / v1_s, used by group B.

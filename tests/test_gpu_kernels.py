@@ -360,6 +360,74 @@ def test_vbsa_half_items_match_oracle(gpu, ear, kn):
     _attn_check(out, ref)
 
 
+_BCHUNK_QSZ = (129, 150, 160, 161, 180, 192, 193, 385, 448, 650, 1, 64, 128, 256)
+_BCHUNK_LEN = (0, 1, 5, 31, 32, 33, 63, 64, 65, 96, 97, 127, 128, 129, 160, 191, 192, 193, 255, 256, 257, 700)
+
+
+def _b_chunked_case(r, h=4):
+    """Last tiles of 129 to 192 queries (group B's two waves per 32 queries take the two 32-key halves of every
+    tile) next to half, full and larger items.  Key clusters of one token each make a map row's stream exactly
+    as long as the number of clusters it selects: lengths on both sides of every 32-key chunk edge, 0 (an empty
+    row) and the whole sequence."""
+    qsz = np.array(_BCHUNK_QSZ, np.int32)
+    s = int(qsz.sum())
+    qn, kn = len(qsz), s
+    qs = np.stack([qsz, qsz[::-1], np.roll(qsz, 5), np.roll(qsz[::-1], 9)][:h])[None]
+    ks = np.ones((1, h, kn), np.int32)
+    m = np.zeros((1, h, qn, kn), bool)
+    lens = _BCHUNK_LEN + (kn,)
+    for b in range(h):
+        for i in range(qn):
+            m[0, b, i, r.choice(kn, size=lens[(i + 9 * b) % len(lens)], replace=False)] = True
+    return h, s, qs, ks, m
+
+
+def test_vbsa_b_chunked_items_match_oracle(gpu):
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd
+
+    say("vbsa B-chunked items")
+    r = np.random.default_rng(100)
+    h, s, qs, ks, m = _b_chunked_case(r)
+    q, qt = rand_bf16((1, h, s, 128), 101, gpu, 0.5)
+    k, kt = rand_bf16((1, h, s, 128), 102, gpu, 0.5)
+    v, vt = rand_bf16((1, h, s, 128), 103, gpu)
+    mt, qst, kst = torch.from_numpy(m).to(gpu), torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu)
+    out = dynamic_block_sparse_fwd(qt, kt, vt, mt, qst, kst)
+    ref = O.block_sparse_attention(q, k, v, m, qs, ks)
+    _attn_check(out, ref)
+    # per query cluster, so that a wrong cluster cannot hide in the whole tensor's cosine
+    o = f32(out)
+    for b in range(h):
+        off = np.concatenate([[0], np.cumsum(qs[0, b])])
+        for i in range(qs.shape[-1]):
+            a, e = int(off[i]), int(off[i + 1])
+            got, want = o[0, b, a:e].astype(np.float64), np.asarray(ref[0, b, a:e], np.float64)
+            assert np.abs(got - want).max(initial=0.0) <= ATTN_MAX_ABS, (b, i, e - a, int(m[0, b, i].sum()))
+            if not m[0, b, i].any():
+                assert np.all(got == 0), (b, i)
+
+
+def test_fused_b_chunked_items_equal_separate_passes(gpu):
+    from svoo_amd.co_clustering import dynamic_block_sparse_fwd, dynamic_block_sparse_fwd_fused
+    from svoo_amd.permute import apply_inverse_permutation_bshd, permute_pair_by_indices
+    from svoo_amd.processor import _permute_rows
+
+    say("fused vbsa B-chunked items")
+    r = np.random.default_rng(105)
+    h, s, qs, ks, m = _b_chunked_case(r)
+    qi = torch.from_numpy(np.stack([r.permutation(s) for _ in range(h)]).astype(np.int32)).to(gpu)
+    ki = torch.from_numpy(np.stack([r.permutation(s) for _ in range(h)]).astype(np.int32)).to(gpu)
+    _, q = rand_bf16((1, h, s, 128), 106, gpu, 0.5)
+    _, k = rand_bf16((1, h, s, 128), 107, gpu, 0.5)
+    _, v = rand_bf16((1, h, s, 128), 108, gpu)
+    mt, qst, kst = torch.from_numpy(m).to(gpu), torch.from_numpy(qs).to(gpu), torch.from_numpy(ks).to(gpu)
+    out = dynamic_block_sparse_fwd_fused(q, k, v, mt, qst, kst, qi, ki)
+    qp = _permute_rows(q, qi)
+    kp, vp = permute_pair_by_indices(k, v, ki)
+    ref = apply_inverse_permutation_bshd(dynamic_block_sparse_fwd(qp, kp, vp, mt, qst, kst), qi)
+    assert torch.equal(out, ref)
+
+
 def test_vbsa_dense_equals_sdpa(gpu):
     from svoo_amd.co_clustering import dynamic_block_sparse_fwd
 
