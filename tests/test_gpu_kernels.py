@@ -526,13 +526,15 @@ def test_vbsa_work_list_over_many_heads(gpu, bh):
 
 def test_vbsa_many_query_clusters_keep_cluster_order(gpu):
     """A head with more than 4096 query clusters is planned in cluster order (the longest-first sort covers
-    up to 4096): one head of 5000 clusters of 1-3 queries, every item a half item, against the oracle."""
+    up to 4096): one head of 5000 clusters, most of 1-3 queries (half items), a few of 150-700 (B-chunked, full
+    and half last tiles), against the oracle."""
     from svoo_amd.co_clustering import dynamic_block_sparse_fwd
 
     say("vbsa 5000 query clusters")
     r = np.random.default_rng(81)
     qn, kn = 5000, 24
     qsz = r.integers(1, 4, qn).astype(np.int32)
+    qsz[[7, 1000, 2500, 4000, 4999]] = [150, 420, 700, 300, 192]
     s = int(qsz.sum())
     cuts = np.sort(r.choice(np.arange(1, s), size=kn - 1, replace=False))
     ks = np.diff(np.concatenate([[0], cuts, [s]])).astype(np.int32)[None, None]
