@@ -429,7 +429,7 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
 }
 
 // --------------------------------------------------------------------------------------- assign
-// Block = 4 waves x 128 tokens (4 MFMA column blocks of 32 per wave); the token rows stay in
+// Block = 4 waves x 32 NCB tokens (NCB MFMA column blocks of 32 per wave); the token rows stay in
 // registers as the MFMA B operand for the whole pass.  E_hi and E_lo stream through LDS in chunks
 // of 64 rows, double buffered and filled by LDS DMA (unpadded rows, XOR-swizzled 16-byte chunks),
 // one barrier per chunk.  Each lane keeps a running argmax over the 16 cluster rows it holds of
@@ -440,10 +440,13 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
 constexpr int kAsgTokWave = 128;
 constexpr int kAsgTok = 4 * kAsgTokWave;
 
-// With LIST the block's tokens are entries [512 x, 512 x + 512) of the head's token list (list[bidx][.],
-// count[bidx] entries; blocks past the count exit at once): the tokens the certified fp16 pass could not
-// settle.
-template <bool LIST>
+// With LIST the block's tokens are entries [T x, T x + T) of the head's token list (T = 128 NCB; list[bidx][.],
+// count[bidx] entries; blocks past the count exit at once): the tokens the certified fp16 pass or the
+// candidate pass could not settle.  Every block streams all of E, so a short list runs fastest on one column
+// block per wave (more blocks, each a quarter of the MFMA work): the candidate passes leave about 0.6% of the
+// keys at C3 from a warm start, one 512-token block per head with four column blocks (80-87 us per pass
+// against 38-41 us with one).  The certified pass's longer lists keep four.
+template <bool LIST, int NCB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi,
                         const uint16_t* __restrict__ e_lo, int32_t* __restrict__ labels, int n, int j, int jpad,
@@ -453,9 +456,10 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   const int bidx = blockIdx.y;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int h = lane / 32, l32 = lane % 32;
-  const int tok0 = blockIdx.x * kAsgTok + wave * kAsgTokWave;
+  constexpr int kTokWave = 32 * NCB, kTokBlock = 4 * kTokWave;
+  const int tok0 = blockIdx.x * kTokBlock + wave * kTokWave;
   const int ntok = LIST ? list_count[(size_t)bidx * kCounterStride] : n;  // positions < ntok hold tokens
-  if (LIST && (int)blockIdx.x * kAsgTok >= ntok) return;
+  if (LIST && (int)blockIdx.x * kTokBlock >= ntok) return;
   const int32_t* lst = LIST ? list + (size_t)bidx * n : nullptr;
   // token at position p of this block's range (positions past the range load a valid row, unused)
   auto token_at = [&](int pos) __attribute__((always_inline)) -> int {
@@ -484,9 +488,9 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   issue(0, 0);
 
   // Token operands: B[k = d][n = token], lane provides 8 consecutive d of token l32 per k-step.
-  u32x4_t xop[4][8];
+  u32x4_t xop[NCB][8];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     const int row = token_at(tok0 + cb * 32 + l32);
     const u32x4_t* src = (const u32x4_t*)(xb + (size_t)row * 128);
 #pragma unroll
@@ -498,9 +502,14 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   const int abase = l32 * 128 + 8 * (h ^ (sw & 1));
 #define AOFF(ks) (abase + 16 * ((ks) ^ g))
 
-  float best_v[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // tagged
-  float best_s[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};  // without the tag
-  int best_j[4] = {0, 0, 0, 0};                                     // tile base row
+  float best_v[NCB], best_s[NCB];  // tagged, without the tag
+  int best_j[NCB];                 // tile base row
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    best_v[cb] = -INFINITY;
+    best_s[cb] = -INFINITY;
+    best_j[cb] = 0;
+  }
 
   for (int c = 0; c < nchunks; ++c) {
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -513,7 +522,7 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
     u32x4_t al = *(const u32x4_t*)(sl + AOFF(0));
 #pragma unroll
     for (int rb = 0; rb < kAssignChunk / 32; ++rb) {
-      f32x16_t acc[4] = {};
+      f32x16_t acc[NCB] = {};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
         const u32x4_t ch = ah, cl = al;
@@ -525,9 +534,9 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
         // keep the next k-step's LDS reads ahead of this step's eight MFMAs
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma32x32x16(as_bf16x8(ch), as_bf16x8(xop[cb][ks]), acc[cb]);
+        for (int cb = 0; cb < NCB; ++cb) acc[cb] = mfma32x32x16(as_bf16x8(ch), as_bf16x8(xop[cb][ks]), acc[cb]);
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma32x32x16(as_bf16x8(cl), as_bf16x8(xop[cb][ks]), acc[cb]);
+        for (int cb = 0; cb < NCB; ++cb) acc[cb] = mfma32x32x16(as_bf16x8(cl), as_bf16x8(xop[cb][ks]), acc[cb]);
       }
       // Argmax over the lane's 16 values of each tile: the low 4 mantissa bits of each score are
       // replaced by 15 - r (a change of at most 2^-19 of the score, below the rounding of the hi + lo
@@ -536,7 +545,7 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
       // Row of slot r is jb + (r/4)*8 + r%4 + 4h, decoded at the end.
       const int jb = c * kAssignChunk + rb * 32;
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
+      for (int cb = 0; cb < NCB; ++cb) {
         float t[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r)
@@ -557,15 +566,15 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   }
 #undef AOFF
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     const int r = 15 - (int)(__float_as_uint(best_v[cb]) & 15u);
     best_j[cb] += (r / 4) * 8 + (r % 4) + h * 4;
   }
-  int lab[4], oldl[4], tokv[4];
-  uint64_t chm[4];
+  int lab[NCB], oldl[NCB], tokv[NCB];
+  uint64_t chm[NCB];
   int nch_wave = 0;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     // the two halves of a token: larger score, then lower row
     const float ov = __shfl_xor(best_s[cb], 32);
     const int oj = __shfl_xor(best_j[cb], 32);
@@ -586,7 +595,7 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   const int cbase = nchanges ? wave_reserve(nchanges, nch_wave) : 0;
   int cpre = 0;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     if (tokv[cb] >= 0) {
       if (oldl[cb] != lab[cb])
         changes[cbase + cpre + mask_rank(chm[cb])] = make_int2(bidx * n + tokv[cb], (oldl[cb] << 16) | lab[cb]);
@@ -1245,9 +1254,12 @@ __global__ void __launch_bounds__(256) cocluster_nu_kernel(const float* __restri
 }
 
 // score: one wave per kCandWaveTok consecutive label-sorted positions, as in the radius kernel: the same
-// anchors, the radii it wrote.  A certified label also becomes the position's anchor for the next pass.  The wave's distinct anchors (usually one or two) bring their lists;
-// the union (a bitmap in the wave's LDS, then compacted in cluster order) is scored on the hi + lo MFMA 32
-// clusters at a time.  One reservation per block and list.
+// anchors, the radii it wrote.  A certified label also becomes the position's anchor for the next pass.  The
+// wave's distinct anchors (usually one or two) bring their lists; the union (a bitmap in the wave's LDS, then
+// compacted in cluster order) is scored on the hi + lo MFMA 32 clusters at a time.  One reservation per block
+// and list.  With SELF, C reaches LDS by DMA issued beside the position loads, so its latency overlaps theirs
+// (a register load, wait and LDS store ahead of them cost a round trip per block: 403 against 370 us per
+// launch at C3), and ||C||_F comes from the reads of the |y| loop.
 template <bool SELF>
 __global__ void __launch_bounds__(256) cocluster_score_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi, const uint16_t* __restrict__ e_lo,
@@ -1263,25 +1275,8 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
   __shared__ int s_cnt[2][4], s_base[2];
   constexpr int kCRows = SELF ? 128 : 1;
   __shared__ __attribute__((aligned(16))) uint16_t s_c[kCRows * 128];
-  __shared__ float s_cf[4];
   const int bidx = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, h = lane / 32,
             l32 = lane % 32;
-  if constexpr (SELF) {
-    // C into LDS (16-byte chunk c of row r at chunk swz(r, c)) and ||C||_F, as in the radius kernel
-    const uint16_t* cb_base = cother + (size_t)bidx * ko * 128;
-    float sq = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + 256 * i, r = c / 16, ch = c % 16;
-      const u32x4_t w = r < ko ? ((const u32x4_t*)cb_base)[c] : u32x4_t{0u, 0u, 0u, 0u};
-      *(u32x4_t*)(s_c + r * 128 + swz(r, ch) * 8) = w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sq = dot2_bf16(w[e], w[e], sq);
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
-    if (lane == 0) s_cf[wave] = sq;
-  }
   const int p0 = blockIdx.x * kCandBlockTok + wave * kCandWaveTok;
   const bool wv = p0 < n;  // the wave has positions (the block's reservations below need every wave)
   uint32_t* bm = s_bm[wave];
@@ -1299,6 +1294,29 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
     anc[cb] = pos_anc[o];
     vt[cb] = inpos[cb] && anc[cb] >= 0 && anc[cb] < j && (SELF || pos_t[o] > 0.0f);
     if (!vt[cb]) anc[cb] = 0;
+  }
+  float nrm_a[TB], tu_a[TB];  // the anchor's profile norm and list radius, requested early
+  if constexpr (SELF) {
+    // C into LDS by DMA (16-byte chunk c of row r at chunk swz(r, c)): wave w fills rows 32 w .. 32 w + 31,
+    // 4 rows (1 KB) per instruction, lane i chunk i % 16 of row 4 g + i / 16 from logical chunk swz(r, i % 16);
+    // rows past ko are written as zeros.  Completion is waited for before the barrier that publishes C.
+    const uint16_t* cb_base = cother + (size_t)bidx * ko * 128;
+    const uint32_t sbase = lds_addr(s_c);
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
+    const int prow = lane / 16, pch = lane % 16;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const int r = 32 * wave + 4 * g + prow;
+      if (r < ko)
+        lds_dma16_asm(cb_base, (uint32_t)(r * 128 + swz(r, pch) * 8) * 2u, sbase + (32 * wu + 4 * g) * 256);
+      else
+        *(u32x4_t*)(s_c + r * 128 + pch * 8) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int cb = 0; cb < TB; ++cb) {
+      nrm_a[cb] = nrm[(size_t)bidx * jpad + anc[cb]];
+      tu_a[cb] = __uint_as_float(tused[(size_t)bidx * jpad + anc[cb]]);
+    }
   }
   // distinct anchors: lane k < nd holds the k-th
   const int myanc = cand_slot<TB>(anc, h, l32);
@@ -1435,10 +1453,11 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
 #pragma unroll
   for (int cb = 0; cb < TB; ++cb) rok[cb] = true;
   if constexpr (SELF) {
-    __syncthreads();  // C is in LDS
-    const float cfro = sqrtf((s_cf[0] + s_cf[1] + s_cf[2] + s_cf[3]) * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's C rows have landed
+    __syncthreads();                                        // C is in LDS
     const float nu = __uint_as_float(nu_bits[bidx]);
     float ysq[TB];
+    float csq = 0.0f;  // ||C||_F^2 from the same reads (each wave reads all of C once)
 #pragma unroll
     for (int cb = 0; cb < TB; ++cb) ysq[cb] = 0.0f;
     if (wv) {
@@ -1447,6 +1466,10 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
         u32x4_t ca[8];
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) ca[ks] = *(const u32x4_t*)(s_c + crow * 128 + swz(crow, ks * 2 + h) * 8);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) csq = dot2_bf16(ca[ks][e], ca[ks][e], csq);
 #pragma unroll
         for (int cb = 0; cb < TB; ++cb) {
           f32x16_t acc = {};
@@ -1457,16 +1480,17 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
         }
       }
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) csq += __shfl_xor(csq, o);
+    const float cfro = sqrtf(csq * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
     float tr[TB];
 #pragma unroll
     for (int cb = 0; cb < TB; ++cb) {
       const float yn = sqrtf(ysq[cb] + __shfl_xor(ysq[cb], 32));
       const float sa = fmaxf(sav[cb], __shfl_xor(sav[cb], 32));
       const float xnu = wv ? sqrtf(xn2[cb] * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f) : 0.0f;
-      tr[cb] = (vt[cb] && sa > -INFINITY) ? cand_radius(sa, yn, xnu, cfro, emax, nrm[(size_t)bidx * jpad + anc[cb]], nu)
-                                          : -1.0f;
-      const float tu = __uint_as_float(tused[(size_t)bidx * jpad + anc[cb]]);
-      rok[cb] = tr[cb] > 0.0f && tr[cb] <= tu;
+      tr[cb] = (vt[cb] && sa > -INFINITY) ? cand_radius(sa, yn, xnu, cfro, emax, nrm_a[cb], nu) : -1.0f;
+      rok[cb] = tr[cb] > 0.0f && tr[cb] <= tu_a[cb];
     }
     // record: one atomic per distinct anchor of the wave
     const int myanc2 = cand_slot<TB>(anc, h, l32);
@@ -1595,16 +1619,20 @@ static int prep_launch(const uint16_t* a, const uint16_t* b, uint16_t* e_hi, uin
   return check_launch("svoo_cocluster_prep");
 }
 
+// short_list: the list is expected to hold a small share of the tokens (the candidate pass's leftovers): one
+// column block per wave.
 static int assign_launch(const uint16_t* x, const uint16_t* e_hi, const uint16_t* e_lo, int32_t* labels, int bh, int n,
                          int j, int jpad, hipStream_t stream, int2* changes = nullptr, int32_t* nchanges = nullptr,
-                         const int32_t* list = nullptr, const int32_t* list_count = nullptr) {
-  dim3 grid((n + kAsgTok - 1) / kAsgTok, bh);
-  if (list)
-    hipLaunchKernelGGL(cocluster_assign_kernel<true>, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad,
-                       changes, nchanges, list, list_count);
+                         const int32_t* list = nullptr, const int32_t* list_count = nullptr, bool short_list = false) {
+  if (list && short_list)
+    hipLaunchKernelGGL((cocluster_assign_kernel<true, 1>), dim3((n + 127) / 128, bh), dim3(256), 0, stream, x, e_hi,
+                       e_lo, labels, n, j, jpad, changes, nchanges, list, list_count);
+  else if (list)
+    hipLaunchKernelGGL((cocluster_assign_kernel<true, 4>), dim3((n + kAsgTok - 1) / kAsgTok, bh), dim3(256), 0, stream,
+                       x, e_hi, e_lo, labels, n, j, jpad, changes, nchanges, list, list_count);
   else
-    hipLaunchKernelGGL(cocluster_assign_kernel<false>, grid, dim3(256), 0, stream, x, e_hi, e_lo, labels, n, j, jpad,
-                       changes, nchanges, nullptr, nullptr);
+    hipLaunchKernelGGL((cocluster_assign_kernel<false, 4>), dim3((n + kAsgTok - 1) / kAsgTok, bh), dim3(256), 0,
+                       stream, x, e_hi, e_lo, labels, n, j, jpad, changes, nchanges, nullptr, nullptr);
   return check_launch("svoo_cocluster_assign");
 }
 
@@ -1881,7 +1909,7 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
         std::swap(t_prev, t_rec);
       }
       if ((r = check_launch("svoo_co_cluster (candidates)"))) return r;
-      r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s, changes, cnt, fb_list, fb_count);
+      r = assign_launch(x, e_hi, e_lo, labels, bh, n, kx, jpad, s, changes, cnt, fb_list, fb_count, true);
     } else if (pr && !first) {
       hipLaunchKernelGGL(cocluster_prune_kernel, dim3((n + 256 * kPruneSub - 1) / (256 * kPruneSub), bh), dim3(256),
                          0, s, labels, bnd, delta, delta_max, n, jpad, plist, list_count);
