@@ -1259,7 +1259,9 @@ __global__ void __launch_bounds__(256) cocluster_nu_kernel(const float* __restri
 // compacted in cluster order) is scored on the hi + lo MFMA 32 clusters at a time.  One reservation per block
 // and list.  With SELF, C reaches LDS by DMA issued beside the position loads, so its latency overlaps theirs
 // (a register load, wait and LDS store ahead of them cost a round trip per block: 403 against 370 us per
-// launch at C3), and ||C||_F comes from the reads of the |y| loop.
+// launch at C3), and ||C||_F comes from the reads of the |y| loop.  The |y| MFMAs run once the union is
+// known, while the first tile's E_hi rows are in flight (after the scores they cost ~6% more per launch);
+// C is read one k-step at a time there, which keeps the kernel at four waves per SIMD.
 template <bool SELF>
 __global__ void __launch_bounds__(256) cocluster_score_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ e_hi, const uint16_t* __restrict__ e_lo,
@@ -1404,20 +1406,56 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
     c1[cb] = -1;
     fin[cb] = true;
   }
-  if (wv && !uover) {
-    const uint16_t* eh = e_hi + (size_t)bidx * jpad * 128;
-    const uint16_t* el = e_lo + (size_t)bidx * jpad * 128;
-    for (int ut = 0; ut * 32 < nu; ++ut) {
-      const int ui = ut * 32 + l32;
-      const int crow = ul[ui < nu ? ui : 0];
-      const u32x4_t* hrow = (const u32x4_t*)(eh + (size_t)crow * 128) + h;
-      const u32x4_t* lrow = (const u32x4_t*)(el + (size_t)crow * 128) + h;
-      u32x4_t ph[8], pl[8];
+  const bool scoring = wv && !uover;
+  const uint16_t* eh = e_hi + (size_t)bidx * jpad * 128;
+  const uint16_t* el = e_lo + (size_t)bidx * jpad * 128;
+  u32x4_t ph[8], pl[8];
+  auto tile_row = [&](int ut) __attribute__((always_inline)) {
+    const int ui = ut * 32 + l32;
+    return (int)ul[ui < nu ? ui : 0];
+  };
+  auto load_hi = [&](int crow) __attribute__((always_inline)) {
+    const u32x4_t* hrow = (const u32x4_t*)(eh + (size_t)crow * 128) + h;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        ph[ks] = hrow[ks * 2];
-        pl[ks] = lrow[ks * 2];
+    for (int ks = 0; ks < 8; ++ks) ph[ks] = hrow[ks * 2];
+  };
+  auto load_lo = [&](int crow) __attribute__((always_inline)) {
+    const u32x4_t* lrow = (const u32x4_t*)(el + (size_t)crow * 128) + h;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) pl[ks] = lrow[ks * 2];
+  };
+  float ysq[TB];
+  float csq = 0.0f;  // SELF: ||C||_F^2 from the |y| loop's reads (each wave reads all of C once)
+#pragma unroll
+  for (int cb = 0; cb < TB; ++cb) ysq[cb] = 0.0f;
+  if constexpr (SELF) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's C rows (and token rows) have landed
+    __syncthreads();                                        // C is in LDS
+    // the first tile's E_hi rows arrive under the |y| work; an empty union (every anchor's list too long)
+    // has no tile, and ul holds nothing written by this block
+    if (scoring && nu > 0) load_hi(tile_row(0));
+    if (wv) {
+      static_assert(TB == 1, "one token block");
+      for (int ct = 0; ct * 32 < ko; ++ct) {
+        const int crow = ct * 32 + l32;
+        f32x16_t acc = {};
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+          const u32x4_t ca = *(const u32x4_t*)(s_c + crow * 128 + swz(crow, ks * 2 + h) * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) csq = dot2_bf16(ca[e], ca[e], csq);
+          acc = mfma32x32x16(as_bf16x8(ca), as_bf16x8(xop[0][ks]), acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ysq[0] = fmaf(acc[r], acc[r], ysq[0]);
       }
+    }
+  }
+  if (scoring) {
+    for (int ut = 0; ut * 32 < nu; ++ut) {
+      const int crow_t = tile_row(ut);
+      if (!SELF || ut > 0) load_hi(crow_t);
+      load_lo(crow_t);
 #pragma unroll
       for (int cb = 0; cb < TB; ++cb) {
         f32x16_t acc = {};
@@ -1453,33 +1491,7 @@ __global__ void __launch_bounds__(256) cocluster_score_kernel(
 #pragma unroll
   for (int cb = 0; cb < TB; ++cb) rok[cb] = true;
   if constexpr (SELF) {
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's C rows have landed
-    __syncthreads();                                        // C is in LDS
     const float nu = __uint_as_float(nu_bits[bidx]);
-    float ysq[TB];
-    float csq = 0.0f;  // ||C||_F^2 from the same reads (each wave reads all of C once)
-#pragma unroll
-    for (int cb = 0; cb < TB; ++cb) ysq[cb] = 0.0f;
-    if (wv) {
-      for (int ct = 0; ct * 32 < ko; ++ct) {
-        const int crow = ct * 32 + l32;
-        u32x4_t ca[8];
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) ca[ks] = *(const u32x4_t*)(s_c + crow * 128 + swz(crow, ks * 2 + h) * 8);
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) csq = dot2_bf16(ca[ks][e], ca[ks][e], csq);
-#pragma unroll
-        for (int cb = 0; cb < TB; ++cb) {
-          f32x16_t acc = {};
-#pragma unroll
-          for (int ks = 0; ks < 8; ++ks) acc = mfma32x32x16(as_bf16x8(ca[ks]), as_bf16x8(xop[cb][ks]), acc);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) ysq[cb] = fmaf(acc[r], acc[r], ysq[cb]);
-        }
-      }
-    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) csq += __shfl_xor(csq, o);
     const float cfro = sqrtf(csq * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
