@@ -483,20 +483,18 @@ def kernel_table(step, cfg, h, nv, d, qcn, kcn, iters):
                           "note": "exact bound test before each later query-side pass"}
     acc = launches("centroid_accumulate_kernel")
     if acc:
-        # the first iteration's two launches sum every token (sorted order); later launches are guarded and
-        # run only when an iteration changes more labels than the incremental update handles well
+        # the first iteration's two launches sum every token (sorted order)
         full = acc[:2]
         acc_bytes = bh * nv * (2 * d + 8) * len(full)
         ach = acc_bytes / (sum(full) * 1e-6) / 1e9
         stage["centroid_accumulate"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
                                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
-                                        "full_pass_avg_us": round(sum(full) / len(full), 2),
-                                        "guarded_launches_avg_us": round(sum(acc[2:]) / len(acc[2:]), 2)
-                                        if len(acc) > 2 else None}
-    dl = launches("centroid_delta_kernel")
-    if dl:
-        stage["centroid_delta"] = {"avg_us": round(sum(dl) / len(dl), 2), "launches": len(dl),
-                                   "note": "moves only the tokens whose label changed"}
+                                        "full_pass_avg_us": round(sum(full) / len(full), 2)}
+    mv = launches("centroid_move_kernel")
+    if mv:
+        stage["centroid_move"] = {"avg_us": round(sum(mv) / len(mv), 2), "launches": len(mv),
+                                  "note": "later iterations: moves only the tokens whose label changed, or "
+                                          "recounts from the sorted labels when many changed (chosen on the device)"}
     out["clustering"] = stage
     return out
 

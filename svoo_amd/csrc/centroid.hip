@@ -13,8 +13,11 @@
 //   is cleared on the way out so the next update starts from zero (or kept, for the delta update).
 // delta: the co-clustering's later iterations move only the rows whose label changed: each wave walks a
 //   piece of the change list, subtracts the rows from their old clusters' sums and adds them to the new
-//   ones' (runs of equal labels summed in registers, then fp64 atomics) and moves the counts.  Under the exponent-span condition above every partial sum is exact,
-//   so the sums equal a full recount bit for bit; beyond it they can differ in the last fp64 bits.
+//   ones' (runs of equal labels summed in registers, then fp64 atomics) and moves the counts.  Under the
+//   exponent-span condition above every partial sum is exact, so the sums equal a full recount bit for bit;
+//   beyond it they can differ in the last fp64 bits.
+// move: one launch for an incremental iteration that runs the delta or, with too many changed tokens, the
+//   accumulation over the freshly sorted labels, chosen on the device from the change count.
 #include "svoo_common.h"
 
 namespace svoo {
@@ -22,16 +25,13 @@ namespace svoo {
 constexpr int kCentPosPerWave = 128;  // two index words per lane
 constexpr int kCentBatch = 16;        // rows in flight per wave (double buffered)
 
-__global__ void __launch_bounds__(256) centroid_accumulate_kernel(const uint32_t* __restrict__ x,
-                                                                  const int32_t* __restrict__ sorted_idx,
-                                                                  const int32_t* __restrict__ sorted_labels,
-                                                                  double* __restrict__ sums, int n, int k,
-                                                                  const int32_t* __restrict__ guard, int limit) {
-  if (guard && *guard <= limit) return;
+// The accumulation of block (bx, b) of the (positions / 512, heads) grid, 4 waves of 256 threads.
+__device__ __forceinline__ void accumulate_rows(const uint32_t* __restrict__ x, const int32_t* __restrict__ sorted_idx,
+                                                const int32_t* __restrict__ sorted_labels, double* __restrict__ sums,
+                                                int n, int k, int bx, int b) {
   // D = 128 fixed: a row is 64 uint32 words (bf16 pairs), one per lane.
-  const int b = blockIdx.y;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int p0 = (blockIdx.x * (blockDim.x / kWave) + wave) * kCentPosPerWave;
+  const int p0 = (bx * 4 + wave) * kCentPosPerWave;
   if (p0 >= n) return;
   const int cnt = min(n - p0, kCentPosPerWave);
   const int32_t* si = sorted_idx + (size_t)b * n + p0;
@@ -89,13 +89,24 @@ __global__ void __launch_bounds__(256) centroid_accumulate_kernel(const uint32_t
   }
 }
 
+__global__ void __launch_bounds__(256) centroid_accumulate_kernel(const uint32_t* __restrict__ x,
+                                                                  const int32_t* __restrict__ sorted_idx,
+                                                                  const int32_t* __restrict__ sorted_labels,
+                                                                  double* __restrict__ sums, int n, int k) {
+  accumulate_rows(x, sorted_idx, sorted_labels, sums, n, k, blockIdx.x, blockIdx.y);
+}
+
+// The finalize also clears zn int32 words at zp (the co-clustering's per-pass counters, which the next
+// pass's prep needs at zero): one launch less per pass.
 __global__ void __launch_bounds__(256) centroid_finalize_kernel(double* __restrict__ sums,
                                                                 const int32_t* __restrict__ sizes,
                                                                 const uint16_t* old_c, uint16_t* new_c,
                                                                 long long total, int d, int keep_sums,
-                                                                int32_t* __restrict__ reset) {
+                                                                int32_t* __restrict__ reset, int32_t* __restrict__ zp,
+                                                                long long zn) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (reset && i == 0) *reset = 0;  // the delta list's counter, consumed by now
+  if (zp && i < zn) zp[i] = 0;
   if (i >= total) return;
   const long long row = i / d;
   const int cnt = sizes[row];
@@ -114,15 +125,6 @@ __global__ void zero_f64_kernel(double* __restrict__ p, long long n) {
   if (i < n) p[i] = 0.0;
 }
 
-// Grid-stride clear that runs only when *guard > limit (a cheap launch when it does not).
-constexpr int kGuardedZeroBlocks = 1024;
-__global__ void zero_f64_guarded_kernel(double* __restrict__ p, long long n, const int32_t* __restrict__ guard,
-                                        int limit) {
-  if (*guard <= limit) return;
-  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
-    p[i] = 0.0;
-}
-
 __global__ void zero_i32_kernel(int32_t* __restrict__ p, long long n) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
@@ -136,16 +138,11 @@ constexpr int kDeltaBatch = 8;      // rows gathered at once per wave
 // neighbouring entries often leave the same cluster or join the same one.  A wave sums a run of equal old (new)
 // labels in registers and adds it with one atomic per element (under the exponent-span condition above every
 // partial sum is exact, so grouping the additions changes nothing).
-__global__ void __launch_bounds__(256) centroid_delta_kernel(const uint32_t* __restrict__ x,
-                                                             const int2* __restrict__ changes,
-                                                             const int32_t* __restrict__ nchanges,
-                                                             double* __restrict__ sums, int32_t* __restrict__ sizes,
-                                                             int n, int k, int limit) {
+// Wave w0 of nw takes its piece of the change list (total entries).
+__device__ __forceinline__ void delta_rows(const uint32_t* __restrict__ x, const int2* __restrict__ changes, int total,
+                                           double* __restrict__ sums, int32_t* __restrict__ sizes, int n, int k, int w0,
+                                           int nw) {
   const int lane = threadIdx.x % kWave;
-  const int w0 = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
-  const int nw = gridDim.x * (blockDim.x / kWave);
-  const int total = *nchanges;
-  if (total > limit) return;  // the full recount handles this iteration
   const int per = (total + nw - 1) / nw;
   const int e0 = w0 * per, e1 = min(total, e0 + per);
   long long kn = -1, ko = -1;  // cluster rows (head * k + label) of the open runs
@@ -188,6 +185,26 @@ __global__ void __launch_bounds__(256) centroid_delta_kernel(const uint32_t* __r
   flush(ko, o0, o1, co);
 }
 
+// An incremental iteration's update: with at most `limit` changed tokens the blocks below kDeltaBlocks move
+// them (delta), else the blocks below nbx * bh recount every cluster from the sorted labels (accumulate; the
+// sort and the cleared sums come from the guarded sort launched before).  One launch instead of two guarded
+// ones.
+__global__ void __launch_bounds__(256) centroid_move_kernel(const uint32_t* __restrict__ x,
+                                                            const int32_t* __restrict__ sorted_idx,
+                                                            const int32_t* __restrict__ sorted_labels,
+                                                            const int2* __restrict__ changes,
+                                                            const int32_t* __restrict__ nchanges,
+                                                            double* __restrict__ sums, int32_t* __restrict__ sizes,
+                                                            int n, int k, int limit, int nbx, int bh) {
+  const int total = *nchanges;
+  const int bid = blockIdx.x;
+  if (total > limit) {
+    if (bid < nbx * bh) accumulate_rows(x, sorted_idx, sorted_labels, sums, n, k, bid % nbx, bid / nbx);
+  } else if (bid < kDeltaBlocks) {
+    delta_rows(x, changes, total, sums, sizes, n, k, bid * 4 + (int)threadIdx.x / kWave, kDeltaBlocks * 4);
+  }
+}
+
 }  // namespace svoo
 
 using namespace svoo;
@@ -204,48 +221,38 @@ int svoo_zero_i32(int32_t* p, long long n, hipStream_t stream) {
   return check_launch("zero_i32");
 }
 
-int svoo_zero_f64_guarded(double* p, long long n, const int32_t* guard, int limit, hipStream_t stream) {
-  if (n <= 0) return SVOO_OK;
-  hipLaunchKernelGGL(zero_f64_guarded_kernel, dim3(kGuardedZeroBlocks), dim3(256), 0, stream, p, n, guard, limit);
-  return check_launch("zero_f64_guarded");
-}
-
-// Moves the listed tokens between the (kept) fp64 sums and counts, then recomputes the centroids;
-// *reset (the list's counter) is cleared by the finalize.  With more than `limit` listed tokens the delta
-// kernel does nothing: the caller has recounted every cluster instead (its guarded sort and sums).
-int svoo_centroid_delta_impl(const uint16_t* x, const int2* changes, const int32_t* nchanges, double* sums,
-                             int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
-                             int32_t* reset, hipStream_t stream, int limit) {
-  hipLaunchKernelGGL(centroid_delta_kernel, dim3(kDeltaBlocks), dim3(256), 0, stream, (const uint32_t*)x, changes,
-                     nchanges, sums, sizes, n, k, limit);
+// An incremental iteration's centroid update (the co-clustering's later passes): the move kernel (delta or
+// recount, chosen on the device from *nchanges against limit), then the centroids; *nchanges is cleared by the
+// finalize, which also clears zn int32 words at zp.
+int svoo_centroid_move_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
+                            const int2* changes, int32_t* nchanges, double* sums, int32_t* sizes, const uint16_t* old_c,
+                            uint16_t* new_c, int bh, int n, int k, int limit, hipStream_t stream, int32_t* zp,
+                            long long zn) {
+  const int nbx = (n + 4 * kCentPosPerWave - 1) / (4 * kCentPosPerWave);
+  const int blocks = max(nbx * bh, kDeltaBlocks);
+  hipLaunchKernelGGL(centroid_move_kernel, dim3(blocks), dim3(256), 0, stream, (const uint32_t*)x, sorted_idx,
+                     sorted_labels, changes, nchanges, sums, sizes, n, k, limit, nbx, bh);
   const long long total = (long long)bh * k * 128;
-  hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, sums,
-                     sizes, old_c, new_c, total, 128, 1, reset);
-  return check_launch("svoo_centroid_delta");
+  const long long fthreads = max(total, zp ? zn : 0ll);
+  hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((fthreads + 255) / 256)), dim3(256), 0, stream, sums,
+                     sizes, old_c, new_c, total, 128, 1, nchanges, zp, zn);
+  return check_launch("svoo_centroid_move");
 }
 
-// sums must be zero on entry; it is zero again on return unless keep_sums.  With a guard the sums are
-// accumulated only when *guard > limit (the finalize is then the caller's).
-void svoo_centroid_accumulate_guarded(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
-                                      double* sums, int bh, int n, int k, const int32_t* guard, int limit,
-                                      hipStream_t stream) {
-  const int pos_per_block = 4 * kCentPosPerWave;
-  dim3 grid((n + pos_per_block - 1) / pos_per_block, bh);
-  hipLaunchKernelGGL(centroid_accumulate_kernel, grid, dim3(256), 0, stream, (const uint32_t*)x, sorted_idx,
-                     sorted_labels, sums, n, k, guard, limit);
-}
-
+// sums must be zero on entry; it is zero again on return unless keep_sums.  The finalize also clears zn int32
+// words at zp.
 int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
                               const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
-                              double* sums, hipStream_t stream, int keep_sums) {
+                              double* sums, hipStream_t stream, int keep_sums, int32_t* zp, long long zn) {
   const int waves_per_block = 4;
   const int pos_per_block = waves_per_block * kCentPosPerWave;
   dim3 grid((n + pos_per_block - 1) / pos_per_block, bh);
   hipLaunchKernelGGL(centroid_accumulate_kernel, grid, dim3(256), 0, stream, (const uint32_t*)x, sorted_idx,
-                     sorted_labels, sums, n, k, (const int32_t*)nullptr, 0);
+                     sorted_labels, sums, n, k);
   const long long total = (long long)bh * k * 128;
-  hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, sums,
-                     sizes, old_c, new_c, total, 128, keep_sums, (int32_t*)nullptr);
+  const long long fthreads = max(total, zp ? zn : 0ll);
+  hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((fthreads + 255) / 256)), dim3(256), 0, stream, sums,
+                     sizes, old_c, new_c, total, 128, keep_sums, (int32_t*)nullptr, zp, zn);
   return check_launch("svoo_centroid_update");
 }
 
@@ -268,5 +275,6 @@ extern "C" int svoo_centroid_update(const uint16_t* x, const int32_t* sorted_idx
   hipStream_t s = (hipStream_t)stream;
   double* sums = (double*)workspace;
   if (int rc = svoo_zero_f64(sums, (long long)bh * k * d, s)) return rc;
-  return svoo_centroid_update_impl(x, sorted_idx, sorted_labels, sizes, old_c, new_c, bh, n, k, sums, s, 0);
+  return svoo_centroid_update_impl(x, sorted_idx, sorted_labels, sizes, old_c, new_c, bh, n, k, sums, s, 0, nullptr,
+                                   0);
 }

@@ -1583,17 +1583,15 @@ using namespace svoo;
 // Forward declarations of the other translation units' internal entry points.
 int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
                            int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
-                           hipStream_t stream, const int32_t* guard = nullptr, int limit = 0);
-void svoo_centroid_accumulate_guarded(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
-                                      double* sums, int bh, int n, int k, const int32_t* guard, int limit,
-                                      hipStream_t stream);
-int svoo_zero_f64_guarded(double* p, long long n, const int32_t* guard, int limit, hipStream_t stream);
+                           hipStream_t stream, const int32_t* guard = nullptr, int limit = 0,
+                           double* zero_sums = nullptr, long long zero_n = 0);
 int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
                               const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
-                              double* sums, hipStream_t stream, int keep_sums = 0);
-int svoo_centroid_delta_impl(const uint16_t* x, const int2* changes, const int32_t* nchanges, double* sums,
-                             int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
-                             int32_t* reset, hipStream_t stream, int limit);
+                              double* sums, hipStream_t stream, int keep_sums, int32_t* zp, long long zn);
+int svoo_centroid_move_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
+                            const int2* changes, int32_t* nchanges, double* sums, int32_t* sizes, const uint16_t* old_c,
+                            uint16_t* new_c, int bh, int n, int k, int limit, hipStream_t stream, int32_t* zp,
+                            long long zn);
 int svoo_zero_i32(int32_t* p, long long n, hipStream_t stream);
 int svoo_zero_f64(double* p, long long n, hipStream_t stream);
 
@@ -1867,6 +1865,8 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
   int rc = svoo_zero_f64(sums_k, (long long)bh * kc * 128, s);
   if (!rc) rc = svoo_zero_f64(sums_q, (long long)bh * qc * 128, s);
   if (!rc) rc = svoo_zero_i32(nch, 2 * kCounterStride, s);
+  // the per-pass counters start at zero; each side's finalize clears them again for the next side's prep
+  if (!rc) rc = svoo_zero_i32((int32_t*)stats, (long long)stats_words, s);
   // One side of an iteration: profiles of x's tokens live in the other side's centroid space.
   // A full iteration sorts the labels and sums every cluster (sums zero on entry, kept on exit); an
   // incremental one lists the tokens whose label changed and moves only their rows between the kept fp64
@@ -1886,7 +1886,6 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
     const bool pr = fp16 && prune;
     // candidate pass: from the second iteration on, over the label order of the last sort
     const bool cp = cand && fp16 && ko <= kCandMaxKp && !first;
-    if (fp16 && (r = svoo_zero_i32((int32_t*)stats, (long long)stats_words, s))) return r;
     if ((r = prep_launch(cent, other, e_hi, e_lo, nullptr, bh, kx, ko, jpad, s, fp16 ? e16 : nullptr, err_max,
                          norm_max, pr ? eold : nullptr, delta, delta_max, t_head, first ? 0 : 1,
                          cp ? praw_k : nullptr, cp ? inv_k : nullptr, cp ? nrm_k : nullptr)))
@@ -1938,17 +1937,18 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
     if (first) {
       if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, sl, counts, nullptr, s)))
         return r;
-      return svoo_centroid_update_impl(x, sorted_idx, sl, sizes, cent, cent, bh, n, kx, sums, s, 1);
+      return svoo_centroid_update_impl(x, sorted_idx, sl, sizes, cent, cent, bh, n, kx, sums, s, 1,
+                                       (int32_t*)stats, (long long)stats_words);
     }
     // More changed tokens than `limit` (a share of all the tokens at which both updates take about the same
-    // time at the Wan shapes): recount every cluster from the sorted labels (guarded kernels, which return at
-    // once otherwise); else move the changed tokens.  The choice is made on the device from the count.
-    if ((r = svoo_zero_f64_guarded(sums, (long long)bh * kx * 128, cnt, limit, s))) return r;
+    // time at the Wan shapes): recount every cluster from the sorted labels (the guarded sort, which returns at
+    // once otherwise, also clears the sums); else move the changed tokens.  The choice is made on the device
+    // from the count, by the sort's kernels and inside the one move launch.
     if ((r = svoo_cluster_sort_impl(labels, bh, n, kx, sorted_idx, sizes, offsets, sl, counts, nullptr, s, cnt,
-                                    limit)))
+                                    limit, sums, (long long)bh * kx * 128)))
       return r;
-    svoo_centroid_accumulate_guarded(x, sorted_idx, sl, sums, bh, n, kx, cnt, limit, s);
-    return svoo_centroid_delta_impl(x, changes, cnt, sums, sizes, cent, cent, bh, n, kx, cnt, s, limit);
+    return svoo_centroid_move_impl(x, sorted_idx, sl, changes, cnt, sums, sizes, cent, cent, bh, n, kx, limit, s,
+                                   (int32_t*)stats, (long long)stats_words);
   };
   // Iteration 1 recounts every cluster from the sorted labels.  Later iterations list the tokens whose label
   // changed; with more than `limit` of them (after a random start, iteration 2 moves 30-90% of the tokens at the

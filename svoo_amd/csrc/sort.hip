@@ -17,11 +17,17 @@ namespace svoo {
 constexpr int kSortChunk = 1024;
 constexpr int kMaxSortClusters = 16384;
 
+// With zs the blocks also clear zn doubles at zs (grid-stride; the sums a recount then accumulates into).
 __global__ void __launch_bounds__(256) sort_hist_kernel(const int32_t* __restrict__ labels, int n, int k,
                                                         int nchunks, int32_t* __restrict__ counts,
                                                         int32_t* __restrict__ err, const int32_t* __restrict__ guard,
-                                                        int limit) {
+                                                        int limit, double* __restrict__ zs, long long zn) {
   if (guard && *guard <= limit) return;
+  if (zs) {
+    const long long step = (long long)gridDim.x * gridDim.y * blockDim.x;
+    for (long long i = ((long long)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < zn; i += step)
+      zs[i] = 0.0;
+  }
   extern __shared__ int32_t hist[];
   const int b = blockIdx.y, c = blockIdx.x;
   for (int i = threadIdx.x; i < k; i += blockDim.x) hist[i] = 0;
@@ -153,15 +159,16 @@ extern "C" size_t svoo_cluster_sort_workspace_size(int bh, int n, int k) {
 
 // Internal entry used by the co-clustering driver: the workspace pointer is already sized.
 // With a guard the three kernels do their work only when *guard > limit (a count on the device; the
-// co-clustering's choice between a full recount and the incremental update).
+// co-clustering's choice between a full recount and the incremental update); then the histogram pass also
+// clears zn doubles at zero_sums when given.
 int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
                            int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
-                           hipStream_t stream, const int32_t* guard, int limit) {
+                           hipStream_t stream, const int32_t* guard, int limit, double* zero_sums, long long zero_n) {
   const int nch = sort_nchunks(n);
   SVOO_REQUIRE((long long)k * nch < (1ll << 31), SVOO_ERR_UNSUPPORTED, "svoo_cluster_sort: k=%d x %d chunks too large",
                k, nch);
   hipLaunchKernelGGL(sort_hist_kernel, dim3(nch, bh), dim3(256), k * sizeof(int32_t), stream, labels, n, k, nch,
-                     counts, err, guard, limit);
+                     counts, err, guard, limit, zero_sums, zero_n);
   int kbits = 0;
   while ((1 << kbits) < k) ++kbits;
   hipLaunchKernelGGL(sort_scan_kernel, dim3(bh), dim3(kScanWaves * kWave), 0, stream, counts, k, nch, sizes, offsets,
@@ -184,5 +191,5 @@ extern "C" int svoo_cluster_sort(const int32_t* labels, int bh, int n, int k, in
   SVOO_REQUIRE(workspace && ws_bytes >= need, SVOO_ERR_WORKSPACE, "svoo_cluster_sort: workspace %zu < %zu",
                ws_bytes, need);
   return svoo_cluster_sort_impl(labels, bh, n, k, sorted_idx, sizes, offsets, sorted_labels, (int32_t*)workspace,
-                                nullptr, (hipStream_t)stream, nullptr, 0);
+                                nullptr, (hipStream_t)stream, nullptr, 0, nullptr, 0);
 }
