@@ -1203,16 +1203,30 @@ __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) r[ks] = brow[ks * 2 + h];
   };
+  // The column constants travel with their tile's rows, one tile ahead: a load issued after the MFMAs and used
+  // at once would also wait for the next tile's rows (loads complete in order), which undid the prefetch.
   u32x4_t bop[8];
-  if (wave < nt) tile_load(bop, wave);
+  double ij = 0.0;
+  float njf = 0.0f;
+  if (wave < nt) {
+    tile_load(bop, wave);
+    ij = ib[wave * 32 + l32];
+    njf = nb[wave * 32 + l32];
+  }
   for (int tj = wave; tj < nt; tj += 4) {
     u32x4_t bnx[8];
-    if (tj + 4 < nt) tile_load(bnx, tj + 4);
+    double ij_n = 0.0;
+    float nj_n = 0.0f;
+    if (tj + 4 < nt) {
+      tile_load(bnx, tj + 4);
+      ij_n = ib[(tj + 4) * 32 + l32];
+      nj_n = nb[(tj + 4) * 32 + l32];
+    }
     f32x16_t acc = {};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) acc = mfma32x32x16(as_bf16x8(aop[ks]), as_bf16x8(bop[ks]), acc);
     const int jj = tj * 32 + l32;
-    const double ij = ib[jj], nj = (double)nb[jj];
+    const double nj = (double)njf;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float d2 = (float)((double)na[r] + nj - 2.0 * ((double)acc[r] * ia[r] * ij) - 0x1p-14);
@@ -1225,6 +1239,8 @@ __global__ void __launch_bounds__(256) cocluster_lists_kernel(const uint16_t* __
     if (tj + 4 < nt) {
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) bop[ks] = bnx[ks];
+      ij = ij_n;
+      njf = nj_n;
     }
   }
   __syncthreads();
