@@ -626,6 +626,10 @@ cocluster_assign_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 // issued from inline assembly; measured with per-wave cycle stamps at C3's key side, the main loop runs at
 // the MFMA rate of two waves per SIMD (about 61 cycles per 32-cycle MFMA and wave), and the token
 // conversion before it and the certification after it take a quarter of a block's time.
+// NCB token blocks of 32 per wave: four for many cluster rows (two waves per SIMD), two for at most 128 rows
+// (the query side, where the pass streams the tokens more than it multiplies: three waves per SIMD, the
+// chunk's two tiles alternating between the accumulator pairs; 196 -> 186 us for the first pass at C3 and
+// 127 -> 121 us per pruned pass).
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
@@ -642,8 +646,8 @@ __device__ __forceinline__ f32x16_t mfma32x32x16_f16(f16x8_t a, f16x8_t b, f32x1
 // next pass needs: certified tokens get their bounds, the others -inf / +inf.  With LIST the block's tokens
 // are entries [512 x, 512 x + 512) of the head's list (list[bidx][.], list_count[bidx * kCounterStride]
 // entries; blocks past the count exit at once).
-template <bool LIST>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <bool LIST, int NCB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NCB == 4 ? 2 : 3, NCB == 4 ? 2 : 3)))
 cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ e16,
                           const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max,
                           int32_t* __restrict__ labels, int n, int j, int jpad, int2* __restrict__ changes,
@@ -656,9 +660,11 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int h = lane / 32, l32 = lane % 32;
-  const int tok0 = blockIdx.x * kAsgTok + wave * kAsgTokWave;
+  static_assert(NCB == 2 || NCB == 4, "two or four column blocks per wave");
+  constexpr int kTokWave = 32 * NCB, kTokBlock = 4 * kTokWave;
+  const int tok0 = blockIdx.x * kTokBlock + wave * kTokWave;
   const int ntok = LIST ? list_count[(size_t)bidx * kCounterStride] : n;  // positions < ntok hold tokens
-  if (LIST && (int)blockIdx.x * kAsgTok >= ntok) return;
+  if (LIST && (int)blockIdx.x * kTokBlock >= ntok) return;
   const int32_t* lst = LIST ? list + (size_t)bidx * n : nullptr;
   // token at position p of this block's range (positions past the range load a valid row, unused)
   auto token_at = [&](int pos) __attribute__((always_inline)) -> int {
@@ -684,16 +690,16 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
 
   // Tokens: fp16, scaled per token.  The previous labels, compared at the end when the changes are listed,
   // are loaded here so that their latency is spent under the pass.
-  int tokv[4], prevl[4], uexp[4];
+  int tokv[NCB], prevl[NCB], uexp[NCB];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     const int pos = tok0 + cb * 32 + l32;
     tokv[cb] = (h == 0 && pos < ntok) ? token_at(pos) : -1;  // -1: no token of this lane
     prevl[cb] = (nchanges && tokv[cb] >= 0) ? labels[(size_t)bidx * n + tokv[cb]] : -1;
   }
-  u32x4_t xop[4][8];
+  u32x4_t xop[NCB][8];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     const int row = token_at(tok0 + cb * 32 + l32);
     const u32x4_t* src = (const u32x4_t*)(xb + (size_t)row * 128);
     u32x4_t raw[8];
@@ -724,10 +730,10 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   const uint16_t* alane = s_e + lane * 8;
 #define AOFF(ks) ((ks) * 512)
 
-  float top1[4], top2[4];
-  int tbase[4];
+  float top1[NCB], top2[NCB];
+  int tbase[NCB];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     top1[cb] = -INFINITY;
     top2[cb] = -INFINITY;
     tbase[cb] = 0;
@@ -735,12 +741,12 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   f32x16_t acc[4];
   // Top-two update of token block cb with tile jb: per score a tag, a median of three and a max (the IEEE
   // maximum builtin: fmaxf on bit-cast values would add a NaN-quieting instruction per score).
-  auto epi = [&](int cb, int jb) __attribute__((always_inline)) {
+  auto epi = [&](int ai, int cb, int jb) __attribute__((always_inline)) {
     const float prev = top1[cb];
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
-      const float ta = __uint_as_float((__float_as_uint(acc[cb][r]) & ~15u) | (uint32_t)(15 - r));
-      const float tb = __uint_as_float((__float_as_uint(acc[cb][r + 1]) & ~15u) | (uint32_t)(14 - r));
+      const float ta = __uint_as_float((__float_as_uint(acc[ai][r]) & ~15u) | (uint32_t)(15 - r));
+      const float tb = __uint_as_float((__float_as_uint(acc[ai][r + 1]) & ~15u) | (uint32_t)(14 - r));
       const float mid = __builtin_amdgcn_fmed3f(top1[cb], ta, tb);
       top1[cb] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(top1[cb], ta), tb);
       top2[cb] = __builtin_elementwise_maximum(top2[cb], mid);
@@ -749,17 +755,18 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   };
   // Two token blocks' MFMAs, their accumulator chains interleaved (a chain's next MFMA waits on the previous),
   // with the A operands (E16 rows of the 32-row tile) read from LDS two k-steps ahead into a ring of three.
-  auto mfmas2 = [&](int cb0, const uint16_t* tile) __attribute__((always_inline)) {
+  // (accumulators a0, a0 + 1 from the token blocks x0, x0 + 1)
+  auto mfmas2 = [&](int a0, int x0, const uint16_t* tile) __attribute__((always_inline)) {
     u32x4_t ring[4];
     ring[0] = *(const u32x4_t*)(tile + AOFF(0));
     ring[1] = *(const u32x4_t*)(tile + AOFF(1));
     ring[2] = *(const u32x4_t*)(tile + AOFF(2));
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      acc[cb0] = mfma32x32x16_f16(as_f16x8(ring[ks % 4]), as_f16x8(xop[cb0][ks]), ks ? acc[cb0] : f32x16_t{});
+      acc[a0] = mfma32x32x16_f16(as_f16x8(ring[ks % 4]), as_f16x8(xop[x0][ks]), ks ? acc[a0] : f32x16_t{});
       if (ks + 3 < 8) ring[(ks + 3) % 4] = *(const u32x4_t*)(tile + AOFF(ks + 3));
-      acc[cb0 + 1] =
-          mfma32x32x16_f16(as_f16x8(ring[ks % 4]), as_f16x8(xop[cb0 + 1][ks]), ks ? acc[cb0 + 1] : f32x16_t{});
+      acc[a0 + 1] =
+          mfma32x32x16_f16(as_f16x8(ring[ks % 4]), as_f16x8(xop[x0 + 1][ks]), ks ? acc[a0 + 1] : f32x16_t{});
     }
   };
   // Software pipeline within the wave: the MFMAs of blocks {0, 1} run while the VALU updates the top two of
@@ -791,26 +798,50 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
     // The last step copies the last chunk again into the free buffer: no branch around the copy.
     issue(min(c + 1, nchunks - 1), (c + 1) & 1);
     const uint16_t* se = alane + (c & 1) * (kAssignChunk * 128);
+    if constexpr (NCB == 4) {
 #pragma unroll
-    for (int rb = 0; rb < kAssignChunk / 32; ++rb) {
-      const uint16_t* tile = se + rb * 32 * 128;
-      const int jb = c * kAssignChunk + rb * 32;
+      for (int rb = 0; rb < kAssignChunk / 32; ++rb) {
+        const uint16_t* tile = se + rb * 32 * 128;
+        const int jb = c * kAssignChunk + rb * 32;
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas2(0, 0, tile);
+        epi(2, 2, pend_jb);
+        epi(3, 3, pend_jb);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas2(2, 2, tile);
+        epi(0, 0, jb);
+        epi(1, 1, jb);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+        pend_jb = jb;
+      }
+    } else {
+      // two column blocks: the chunk's two tiles alternate between accumulators {0, 1} and {2, 3}, so a tile's
+      // MFMAs still run beside the top-two updates of the tile before it, in tile order
+      static_assert(kAssignChunk == 64, "two tiles per chunk");
+      const int jb0 = c * kAssignChunk;
       __builtin_amdgcn_sched_barrier(0);
-      mfmas2(0, tile);
-      epi(2, pend_jb);
-      epi(3, pend_jb);
+      mfmas2(0, 0, se);
+      epi(2, 0, pend_jb);
+      epi(3, 1, pend_jb);
       interleave();
       __builtin_amdgcn_sched_barrier(0);
-      mfmas2(2, tile);
-      epi(0, jb);
-      epi(1, jb);
+      mfmas2(2, 0, se + 32 * 128);
+      epi(0, 0, jb0);
+      epi(1, 1, jb0);
       interleave();
       __builtin_amdgcn_sched_barrier(0);
-      pend_jb = jb;
+      pend_jb = jb0 + 32;
     }
   }
-  epi(2, pend_jb);
-  epi(3, pend_jb);
+  if constexpr (NCB == 4) {
+    epi(2, 2, pend_jb);
+    epi(3, 3, pend_jb);
+  } else {
+    epi(2, 0, pend_jb);
+    epi(3, 1, pend_jb);
+  }
 #undef AOFF
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the extra copy lands before the block ends
   const float dd = __uint_as_float(err_max[bidx]), em = __uint_as_float(norm_max[bidx]);
@@ -820,7 +851,7 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   uint64_t fbm[4], chm[4];
   int nfb = 0, nch_wave = 0;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     // |x~| of the fp16 operands themselves: fp32 sums of exact fp16 squares, two per v_dot2_f32_f16 (at most
     // two roundings per step over 64 steps; 1.001 below covers them)
     float n2 = 0.0f;
@@ -886,7 +917,7 @@ cocluster_assign16_kernel(const uint16_t* __restrict__ x, const uint16_t* __rest
   }
   int fpre = 0, cpre = 0;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     const int tok = tokv[cb];
     if (minev[cb] && !certv[cb]) fb_list[(size_t)bidx * n + fbase + fpre + mask_rank(fbm[cb])] = tok;
     if (minev[cb] && certv[cb]) {
@@ -1669,13 +1700,26 @@ static int assign16_launch(const uint16_t* x, const uint16_t* e16, const uint16_
                            int jpad, int32_t* fb_list, int32_t* fb_count, hipStream_t stream, int2* changes,
                            int32_t* nchanges, float* bnd = nullptr, const int32_t* t_head = nullptr,
                            const int32_t* list = nullptr, const int32_t* list_count = nullptr) {
-  dim3 grid((n + kAsgTok - 1) / kAsgTok, bh);
-  if (list)
-    hipLaunchKernelGGL(cocluster_assign16_kernel<true>, grid, dim3(256), 0, stream, x, e16, err_max, norm_max, labels,
-                       n, j, jpad, changes, nchanges, fb_list, fb_count, bnd, t_head, list, list_count);
-  else
-    hipLaunchKernelGGL(cocluster_assign16_kernel<false>, grid, dim3(256), 0, stream, x, e16, err_max, norm_max,
-                       labels, n, j, jpad, changes, nchanges, fb_list, fb_count, bnd, t_head, nullptr, nullptr);
+  // few cluster rows (the query side): two column blocks per wave and four waves per SIMD
+  if (jpad <= 128) {
+    dim3 grid((n + 255) / 256, bh);
+    if (list)
+      hipLaunchKernelGGL((cocluster_assign16_kernel<true, 2>), grid, dim3(256), 0, stream, x, e16, err_max, norm_max,
+                         labels, n, j, jpad, changes, nchanges, fb_list, fb_count, bnd, t_head, list, list_count);
+    else
+      hipLaunchKernelGGL((cocluster_assign16_kernel<false, 2>), grid, dim3(256), 0, stream, x, e16, err_max,
+                         norm_max, labels, n, j, jpad, changes, nchanges, fb_list, fb_count, bnd, t_head, nullptr,
+                         nullptr);
+  } else {
+    dim3 grid((n + kAsgTok - 1) / kAsgTok, bh);
+    if (list)
+      hipLaunchKernelGGL((cocluster_assign16_kernel<true, 4>), grid, dim3(256), 0, stream, x, e16, err_max, norm_max,
+                         labels, n, j, jpad, changes, nchanges, fb_list, fb_count, bnd, t_head, list, list_count);
+    else
+      hipLaunchKernelGGL((cocluster_assign16_kernel<false, 4>), grid, dim3(256), 0, stream, x, e16, err_max,
+                         norm_max, labels, n, j, jpad, changes, nchanges, fb_list, fb_count, bnd, t_head, nullptr,
+                         nullptr);
+  }
   if (int rc = check_launch("svoo_co_cluster (fp16 assign)")) return rc;
   return assign_launch(x, e_hi, e_lo, labels, bh, n, j, jpad, stream, changes, nchanges, fb_list, fb_count);
 }
