@@ -1082,8 +1082,10 @@ constexpr int kCandBlockTok = 4 * kCandWaveTok;
 // position is pos_anc (the sorted labels of the last sort, moved along by the score kernel's certified
 // labels).  Writes, per position, the radius (or -1) and the cluster maxima to trad (float bits, zero on
 // entry), one atomic per distinct anchor of a wave.  C is staged in LDS once per block (16-byte chunk c of
-// row r at chunk swz(r, c)).
-__global__ void __launch_bounds__(256) cocluster_radius_kernel(
+// row r at chunk swz(r, c)) by DMA issued beside the position loads, the anchor rows are requested before the
+// barrier that publishes C, and the kernel runs four waves per SIMD (112 registers, the LDS allows four
+// blocks per CU): 293 -> 264 us per launch at C3 for the first two, 230 us with the third.
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) cocluster_radius_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ cother, const uint16_t* __restrict__ e_hi,
     const uint16_t* __restrict__ e_lo, const float* __restrict__ nrm, const uint32_t* __restrict__ nu_bits,
     const uint32_t* __restrict__ err_max, const uint32_t* __restrict__ norm_max, const int32_t* __restrict__ t_head,
@@ -1091,7 +1093,6 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
     float* __restrict__ pos_t, uint32_t* __restrict__ trad) {
   constexpr int TB = kCandTB;
   __shared__ __attribute__((aligned(16))) uint16_t s_c[128 * 128];
-  __shared__ float s_cf[4];
   const int bidx = blockIdx.y, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave, h = lane / 32,
             l32 = lane % 32;
   const int p0 = blockIdx.x * kCandBlockTok + wave * kCandWaveTok;
@@ -1105,19 +1106,20 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
     tok[cb] = sorted_idx[o];
     anc[cb] = pos_anc[o];
   }
+  // C into LDS by DMA beside the position loads (as in the score kernel): wave w fills rows 32 w .. 32 w + 31,
+  // rows past ko are written as zeros; waited for before the barrier that publishes C
   {
-    float sq = 0.0f;
+    const uint32_t sbase = lds_addr(s_c);
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
+    const int prow = lane / 16, pch = lane % 16;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = tid + 256 * i, r = c / 16, ch = c % 16;
-      const u32x4_t w = r < ko ? ((const u32x4_t*)cb_base)[c] : u32x4_t{0u, 0u, 0u, 0u};
-      *(u32x4_t*)(s_c + r * 128 + swz(r, ch) * 8) = w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sq = dot2_bf16(w[e], w[e], sq);
+    for (int g = 0; g < 8; ++g) {
+      const int r = 32 * wave + 4 * g + prow;
+      if (r < ko)
+        lds_dma16_asm(cb_base, (uint32_t)(r * 128 + swz(r, pch) * 8) * 2u, sbase + (32 * wu + 4 * g) * 256);
+      else
+        *(u32x4_t*)(s_c + r * 128 + pch * 8) = u32x4_t{0u, 0u, 0u, 0u};
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
-    if (lane == 0) s_cf[wave] = sq;
   }
 #pragma unroll
   for (int cb = 0; cb < TB; ++cb) {
@@ -1127,10 +1129,8 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
   u32x4_t xop[TB][8];
   float xn2[TB];
   cand_tokens<TB>(x + (size_t)bidx * n * 128, tok, h, xop, xn2);
-  __syncthreads();
-  if (p0 >= n) return;
-  const float cfro = sqrtf((s_cf[0] + s_cf[1] + s_cf[2] + s_cf[3]) * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
-  // anchor scores on v_dot2_f32_bf16: the lane's 64 components of x against E_hi + E_lo of the anchor
+  // anchor scores on v_dot2_f32_bf16: the lane's 64 components of x against E_hi + E_lo of the anchor (before
+  // the barrier, so the anchor rows' latency overlaps the token rows')
   float sa[TB];
 #pragma unroll
   for (int cb = 0; cb < TB; ++cb) {
@@ -1145,6 +1145,10 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
     }
     sa[cb] = acc + __shfl_xor(acc, 32);
   }
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's C rows have landed
+  __syncthreads();
+  if (p0 >= n) return;
+  float csq = 0.0f;  // ||C||_F^2 from the |y| loop's reads (each wave reads all of C once)
   // |y|^2 on the MFMA (C rows past ko are zero)
   float ysq[TB];
 #pragma unroll
@@ -1155,6 +1159,10 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) ca[ks] = *(const u32x4_t*)(s_c + crow * 128 + swz(crow, ks * 2 + h) * 8);
 #pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) csq = dot2_bf16(ca[ks][e], ca[ks][e], csq);
+#pragma unroll
     for (int cb = 0; cb < TB; ++cb) {
       f32x16_t acc = {};
 #pragma unroll
@@ -1163,6 +1171,9 @@ __global__ void __launch_bounds__(256) cocluster_radius_kernel(
       for (int r = 0; r < 16; ++r) ysq[cb] = fmaf(acc[r], acc[r], ysq[cb]);
     }
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) csq += __shfl_xor(csq, o);
+  const float cfro = sqrtf(csq * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
   const float emax = cand_emax(norm_max, err_max, t_head, bidx);
   const float nu = __uint_as_float(nu_bits[bidx]);
   float tr[TB];
