@@ -1643,6 +1643,11 @@ int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t*
                            int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
                            hipStream_t stream, const int32_t* guard = nullptr, int limit = 0,
                            double* zero_sums = nullptr, long long zero_n = 0);
+int svoo_cluster_sort2_impl(const int32_t* labels_a, int k_a, int32_t* sorted_idx_a, int32_t* sizes_a,
+                            int32_t* offsets_a, int32_t* sorted_labels_a, int32_t* counts_a, const int32_t* labels_b,
+                            int k_b, int32_t* sorted_idx_b, int32_t* sizes_b, int32_t* offsets_b,
+                            int32_t* sorted_labels_b, int32_t* counts_b, int bh, int n, hipStream_t stream);
+extern "C" size_t svoo_cluster_sort_workspace_size(int bh, int n, int k);
 int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, const int32_t* sorted_labels,
                               const int32_t* sizes, const uint16_t* old_c, uint16_t* new_c, int bh, int n, int k,
                               double* sums, hipStream_t stream, int keep_sums, int32_t* zp, long long zn);
@@ -2034,9 +2039,17 @@ extern "C" int svoo_co_cluster(const uint16_t* q, const uint16_t* k, int bh, int
       break;
   }
   // The stable sort of the final labels (the first iteration's sort already is when max_iters == 1).
+  // The two sides' final sorts are independent: one set of three launches, the query side's counts in the change
+  // list's buffer (consumed by now); their sorted labels are not needed.
   if (rc == SVOO_OK && max_iters > 1) {
-    rc = svoo_cluster_sort_impl(k_labels, bh, n, kc, k_sorted_idx, k_sizes, k_offsets, slab, counts, nullptr, s);
-    if (!rc) rc = svoo_cluster_sort_impl(q_labels, bh, n, qc, q_sorted_idx, q_sizes, q_offsets, slab, counts, nullptr, s);
+    if (svoo_cluster_sort_workspace_size(bh, n, qc) <= (size_t)bh * n * sizeof(int2)) {
+      rc = svoo_cluster_sort2_impl(k_labels, kc, k_sorted_idx, k_sizes, k_offsets, nullptr, counts, q_labels, qc,
+                                   q_sorted_idx, q_sizes, q_offsets, nullptr, (int32_t*)changes, bh, n, s);
+    } else {
+      rc = svoo_cluster_sort_impl(k_labels, bh, n, kc, k_sorted_idx, k_sizes, k_offsets, nullptr, counts, nullptr, s);
+      if (!rc)
+        rc = svoo_cluster_sort_impl(q_labels, bh, n, qc, q_sorted_idx, q_sizes, q_offsets, nullptr, counts, nullptr, s);
+    }
   }
   return rc;
 }

@@ -19,9 +19,20 @@ namespace svoo {
 constexpr int kSortChunk = 1024;
 constexpr int kMaxSortClusters = 16384;
 
+// One sort of a launch: a launch sorts the rows of one or two of them (rows [0, bh_a) the first, the rest the
+// second), so that two independent sorts share their three launches.
+struct SortSide {
+  const int32_t* labels;
+  int32_t* counts;
+  int32_t* sizes;
+  int32_t* offsets;
+  int32_t* sorted_idx;
+  int32_t* sorted_labels;
+  int k, kbits;
+};
+
 // With zs the blocks also clear zn doubles at zs (grid-stride; the sums a recount then accumulates into).
-__global__ void __launch_bounds__(256) sort_hist_kernel(const int32_t* __restrict__ labels, int n, int k,
-                                                        int nchunks, int32_t* __restrict__ counts,
+__global__ void __launch_bounds__(256) sort_hist_kernel(SortSide sa, SortSide sb, int bh_a, int n, int nchunks,
                                                         int32_t* __restrict__ err, const int32_t* __restrict__ guard,
                                                         int limit, double* __restrict__ zs, long long zn) {
   if (guard && *guard <= limit) return;
@@ -31,10 +42,13 @@ __global__ void __launch_bounds__(256) sort_hist_kernel(const int32_t* __restric
       zs[i] = 0.0;
   }
   extern __shared__ int32_t hist[];
-  const int b = blockIdx.y, c = blockIdx.x;
+  const bool second = (int)blockIdx.y >= bh_a;
+  const SortSide& S = second ? sb : sa;
+  const int b = second ? blockIdx.y - bh_a : blockIdx.y, c = blockIdx.x, k = S.k;
+  int32_t* counts = S.counts;
   for (int i = threadIdx.x; i < k; i += blockDim.x) hist[i] = 0;
   __syncthreads();
-  const int32_t* lab = labels + (size_t)b * n;
+  const int32_t* lab = S.labels + (size_t)b * n;
   const int s = c * kSortChunk, e = min(n, s + kSortChunk);
   bool bad = false;
   for (int t = s + threadIdx.x; t < e; t += blockDim.x) {
@@ -64,13 +78,17 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 // counts [chunk][cluster] -> bases (in place): base of (chunk c, cluster i) = offset of cluster i + the counts of
 // cluster i in chunks before c, which is the stable order (cluster, then token).  One thread per cluster, 1024
 // clusters per pass; every access of a chunk row is contiguous over the threads.
-__global__ void __launch_bounds__(kScanWaves * kWave) sort_scan_kernel(int32_t* __restrict__ counts, int k,
-                                                                       int nchunks, int32_t* __restrict__ sizes,
-                                                                       int32_t* __restrict__ offsets,
+__global__ void __launch_bounds__(kScanWaves * kWave) sort_scan_kernel(SortSide sa, SortSide sb, int bh_a, int nchunks,
                                                                        const int32_t* __restrict__ guard, int limit) {
   if (guard && *guard <= limit) return;
   __shared__ int wsum[kScanWaves];
-  const int b = blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const bool second = (int)blockIdx.x >= bh_a;
+  const SortSide& S = second ? sb : sa;
+  const int k = S.k;
+  int32_t* counts = S.counts;
+  int32_t* sizes = S.sizes;
+  int32_t* offsets = S.offsets;
+  const int b = second ? blockIdx.x - bh_a : blockIdx.x, tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   int32_t* cnt = counts + (size_t)b * k * nchunks;
   int carry = 0;  // clusters of the earlier passes
   for (int i0 = 0; i0 < k; i0 += kScanWaves * kWave) {
@@ -106,31 +124,31 @@ __global__ void __launch_bounds__(kScanWaves * kWave) sort_scan_kernel(int32_t* 
   }
 }
 
-__global__ void __launch_bounds__(64) sort_scatter_kernel(const int32_t* __restrict__ labels, int n, int k,
-                                                          int kbits, int nchunks, const int32_t* __restrict__ bases,
-                                                          int32_t* __restrict__ sorted_idx,
-                                                          int32_t* __restrict__ sorted_labels,
-                                                          const int32_t* __restrict__ guard, int limit, int bh8) {
+__global__ void __launch_bounds__(64) sort_scatter_kernel(SortSide sa, SortSide sb, int bh_a, int rows, int n,
+                                                          int nchunks, const int32_t* __restrict__ guard, int limit) {
   if (guard && *guard <= limit) return;
   extern __shared__ int32_t base[];
-  // XCD-aware order: workgroup L runs on XCD L % 8, so with bh a multiple of 8 head b's chunks all go to XCD
-  // b % 8 and the scattered writes of a cluster's output lines merge in one L2
-  int b, c;
+  // XCD-aware order: workgroup L runs on XCD L % 8, so with the row count a multiple of 8 row y's chunks all go
+  // to XCD y % 8 and the scattered writes of a cluster's output lines merge in one L2
+  int y, c;
   const int L = blockIdx.x, lane = threadIdx.x;
-  if (bh8) {
+  if (rows % 8 == 0) {
     const int xcd = L % 8, sl = L / 8;
-    b = (sl / nchunks) * 8 + xcd;
+    y = (sl / nchunks) * 8 + xcd;
     c = sl % nchunks;
   } else {
-    b = L / nchunks;
+    y = L / nchunks;
     c = L % nchunks;
   }
-  const int32_t* bs = bases + (size_t)b * k * nchunks;
+  const bool second = y >= bh_a;
+  const SortSide& S = second ? sb : sa;
+  const int b = second ? y - bh_a : y, k = S.k, kbits = S.kbits;
+  const int32_t* bs = S.counts + (size_t)b * k * nchunks;
   for (int i = lane; i < k; i += kWave) base[i] = bs[(size_t)c * k + i];
   __syncthreads();
-  const int32_t* lab = labels + (size_t)b * n;
-  int32_t* out = sorted_idx + (size_t)b * n;
-  int32_t* outl = sorted_labels ? sorted_labels + (size_t)b * n : nullptr;
+  const int32_t* lab = S.labels + (size_t)b * n;
+  int32_t* out = S.sorted_idx + (size_t)b * n;
+  int32_t* outl = S.sorted_labels ? S.sorted_labels + (size_t)b * n : nullptr;
   const int s = c * kSortChunk, e = min(n, s + kSortChunk);
   const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int t0 = s; t0 < e; t0 += kWave) {
@@ -174,21 +192,46 @@ extern "C" size_t svoo_cluster_sort_workspace_size(int bh, int n, int k) {
 // With a guard the three kernels do their work only when *guard > limit (a count on the device; the
 // co-clustering's choice between a full recount and the incremental update); then the histogram pass also
 // clears zn doubles at zero_sums when given.
+static SortSide sort_side(const int32_t* labels, int k, int32_t* sorted_idx, int32_t* sizes, int32_t* offsets,
+                          int32_t* sorted_labels, int32_t* counts) {
+  int kbits = 0;
+  while ((1 << kbits) < k) ++kbits;
+  return SortSide{labels, counts, sizes, offsets, sorted_idx, sorted_labels, k, kbits};
+}
+
+static int sort_launch(const SortSide& sa, const SortSide& sb, int bh_a, int bh_b, int n, int32_t* err,
+                       hipStream_t stream, const int32_t* guard, int limit, double* zero_sums, long long zero_n) {
+  const int nch = sort_nchunks(n), rows = bh_a + bh_b, kmax = max(sa.k, bh_b ? sb.k : 0);
+  SVOO_REQUIRE((long long)kmax * nch < (1ll << 31), SVOO_ERR_UNSUPPORTED,
+               "svoo_cluster_sort: k=%d x %d chunks too large", kmax, nch);
+  hipLaunchKernelGGL(sort_hist_kernel, dim3(nch, rows), dim3(256), kmax * sizeof(int32_t), stream, sa, sb, bh_a, n,
+                     nch, err, guard, limit, zero_sums, zero_n);
+  hipLaunchKernelGGL(sort_scan_kernel, dim3(rows), dim3(kScanWaves * kWave), 0, stream, sa, sb, bh_a, nch, guard,
+                     limit);
+  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nch * rows), dim3(64), kmax * sizeof(int32_t), stream, sa, sb, bh_a,
+                     rows, n, nch, guard, limit);
+  return check_launch("svoo_cluster_sort");
+}
+
+// Internal entry used by the co-clustering driver: the workspace pointer is already sized.
+// With a guard the three kernels do their work only when *guard > limit (a count on the device; the
+// co-clustering's choice between a full recount and the incremental update); then the histogram pass also
+// clears zn doubles at zero_sums when given.
 int svoo_cluster_sort_impl(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
                            int32_t* offsets, int32_t* sorted_labels, int32_t* counts, int32_t* err,
                            hipStream_t stream, const int32_t* guard, int limit, double* zero_sums, long long zero_n) {
-  const int nch = sort_nchunks(n);
-  SVOO_REQUIRE((long long)k * nch < (1ll << 31), SVOO_ERR_UNSUPPORTED, "svoo_cluster_sort: k=%d x %d chunks too large",
-               k, nch);
-  hipLaunchKernelGGL(sort_hist_kernel, dim3(nch, bh), dim3(256), k * sizeof(int32_t), stream, labels, n, k, nch,
-                     counts, err, guard, limit, zero_sums, zero_n);
-  int kbits = 0;
-  while ((1 << kbits) < k) ++kbits;
-  hipLaunchKernelGGL(sort_scan_kernel, dim3(bh), dim3(kScanWaves * kWave), 0, stream, counts, k, nch, sizes, offsets,
-                     guard, limit);
-  hipLaunchKernelGGL(sort_scatter_kernel, dim3(nch * bh), dim3(64), k * sizeof(int32_t), stream, labels, n, k, kbits,
-                     nch, counts, sorted_idx, sorted_labels, guard, limit, (bh % 8) == 0 ? 1 : 0);
-  return check_launch("svoo_cluster_sort");
+  const SortSide sa = sort_side(labels, k, sorted_idx, sizes, offsets, sorted_labels, counts);
+  return sort_launch(sa, sa, bh, 0, n, err, stream, guard, limit, zero_sums, zero_n);
+}
+
+// Two independent sorts of bh rows each (their own counts workspaces) in one set of three launches.
+int svoo_cluster_sort2_impl(const int32_t* labels_a, int k_a, int32_t* sorted_idx_a, int32_t* sizes_a,
+                            int32_t* offsets_a, int32_t* sorted_labels_a, int32_t* counts_a, const int32_t* labels_b,
+                            int k_b, int32_t* sorted_idx_b, int32_t* sizes_b, int32_t* offsets_b,
+                            int32_t* sorted_labels_b, int32_t* counts_b, int bh, int n, hipStream_t stream) {
+  const SortSide sa = sort_side(labels_a, k_a, sorted_idx_a, sizes_a, offsets_a, sorted_labels_a, counts_a);
+  const SortSide sb = sort_side(labels_b, k_b, sorted_idx_b, sizes_b, offsets_b, sorted_labels_b, counts_b);
+  return sort_launch(sa, sb, bh, bh, n, nullptr, stream, nullptr, 0, nullptr, 0);
 }
 
 extern "C" int svoo_cluster_sort(const int32_t* labels, int bh, int n, int k, int32_t* sorted_idx, int32_t* sizes,
