@@ -356,31 +356,52 @@ __global__ void __launch_bounds__(256) cocluster_prep_mfma_kernel(const uint16_t
   // Lane l with l % 32 < 16 holds row r = l % 16 at columns dd0 + 8 (v / 4) + 4 (l / 32) + v % 4 (v = 0..15).
   float err2 = 0.0f, nrm2 = 0.0f, dl2 = 0.0f;
   const int rr = lane % 16, row = r0 + rr;
+  // Slots 4q .. 4q + 3 are four consecutive columns: each array gets one 8-byte store per group (the fp64 copy
+  // two 16-byte accesses) instead of four 2-byte (8-byte) ones.
   if ((lane % 32) < 16 && row < jpad) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int dd = dd0 + 8 * (v / 4) + 4 * (lane / 32) + v % 4;
-      const double e = (double)acc3[v] * inv[rr];
-      const uint16_t hi = f32_to_bf16((float)e);
-      const uint16_t lo = f32_to_bf16((float)(e - (double)bf16_to_f32(hi)));
-      hb[(size_t)row * 128 + dd] = hi;
-      lb[(size_t)row * 128 + dd] = lo;
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int dd = dd0 + 8 * q4 + 4 * (lane / 32);
+      uint16_t hi[4], lo[4], h16b[4];
+      double ev[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const double e = (double)acc3[4 * q4 + i] * inv[rr];
+        ev[i] = e;
+        hi[i] = f32_to_bf16((float)e);
+        lo[i] = f32_to_bf16((float)(e - (double)bf16_to_f32(hi[i])));
+      }
+      *(uint2*)(hb + (size_t)row * 128 + dd) =
+          make_uint2(hi[0] | ((uint32_t)hi[1] << 16), hi[2] | ((uint32_t)hi[3] << 16));
+      *(uint2*)(lb + (size_t)row * 128 + dd) =
+          make_uint2(lo[0] | ((uint32_t)lo[1] << 16), lo[2] | ((uint32_t)lo[3] << 16));
       if (e16) {
-        // padding rows (row >= j) are zero in the fp16 copy: their score is exactly 0
-        const double es = row < j ? ldexp(e, t_scale) : 0.0;
-        const _Float16 h16 = (_Float16)(float)es;
-        const double err = es - (double)(float)h16;  // exact
-        err2 += (float)(err * err);
-        nrm2 += (float)((double)(float)h16 * (double)(float)h16);
-        e16[(size_t)bidx * jpad * 128 + e16_offset(row, dd)] = __builtin_bit_cast(uint16_t, h16);
-        if (e_old) {
-          // change of E since the previous call on this buffer (for the pruning bounds), then keep this E
-          double* eo = e_old + ((size_t)bidx * jpad + row) * 128 + dd;
-          if (have_old) {
-            const double df = e - *eo;
+        double old[4];
+        double* eo = e_old ? e_old + ((size_t)bidx * jpad + row) * 128 + dd : nullptr;
+        if (eo && have_old) {
+          const double2 o01 = *(const double2*)eo, o23 = *(const double2*)(eo + 2);
+          old[0] = o01.x, old[1] = o01.y, old[2] = o23.x, old[3] = o23.y;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // padding rows (row >= j) are zero in the fp16 copy: their score is exactly 0
+          const double es = row < j ? ldexp(ev[i], t_scale) : 0.0;
+          const _Float16 h16 = (_Float16)(float)es;
+          const double err = es - (double)(float)h16;  // exact
+          err2 += (float)(err * err);
+          nrm2 += (float)((double)(float)h16 * (double)(float)h16);
+          h16b[i] = __builtin_bit_cast(uint16_t, h16);
+          if (eo && have_old) {
+            // change of E since the previous call on this buffer (for the pruning bounds)
+            const double df = ev[i] - old[i];
             dl2 += (float)(df * df);
           }
-          *eo = e;
+        }
+        *(uint2*)(e16 + (size_t)bidx * jpad * 128 + e16_offset(row, dd)) =
+            make_uint2(h16b[0] | ((uint32_t)h16b[1] << 16), h16b[2] | ((uint32_t)h16b[3] << 16));
+        if (eo) {  // keep this E
+          *(double2*)eo = make_double2(ev[0], ev[1]);
+          *(double2*)(eo + 2) = make_double2(ev[2], ev[3]);
         }
       }
     }
