@@ -9,7 +9,8 @@
 //   does not depend on the order of the atomics.  Beyond that the fp64 sums round and the last bits can
 //   depend on that order.  The wave's indices and labels arrive in two vector loads; rows are then
 //   fetched 16 at a time, one batch ahead of the accumulation.
-// finalize: centroid = bf16(f32(sum) / f32(size)), size 0 keeps the old centroid; the sum buffer
+// finalize: centroid = bf16(f32(sum) / f32(size)), size 0 keeps the old centroid (four elements of a row per
+//   thread: 16-byte sum loads, one 8-byte store); the sum buffer
 //   is cleared on the way out so the next update starts from zero (or kept, for the delta update).
 // delta: the co-clustering's later iterations move only the rows whose label changed: each wave walks a
 //   piece of the change list, subtracts the rows from their old clusters' sums and adds them to the new
@@ -104,20 +105,29 @@ __global__ void __launch_bounds__(256) centroid_finalize_kernel(double* __restri
                                                                 long long total, int d, int keep_sums,
                                                                 int32_t* __restrict__ reset, int32_t* __restrict__ zp,
                                                                 long long zn) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (reset && i == 0) *reset = 0;  // the delta list's counter, consumed by now
-  if (zp && i < zn) zp[i] = 0;
+  // four consecutive elements of one row per thread (d is a multiple of 4)
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (reset && t == 0) *reset = 0;  // the delta list's counter, consumed by now
+  if (zp && t < zn) zp[t] = 0;
+  const long long i = 4 * t;
   if (i >= total) return;
   const long long row = i / d;
   const int cnt = sizes[row];
-  const double s = sums[i];
-  if (!keep_sums) sums[i] = 0.0;
-  if (cnt > 0) {
-    const float mean = (float)s / (float)cnt;
-    new_c[i] = f32_to_bf16(mean);
-  } else {
-    new_c[i] = old_c[i];
+  double2* sp = (double2*)(sums + i);
+  const double2 s01 = sp[0], s23 = sp[1];
+  if (!keep_sums) {
+    sp[0] = make_double2(0.0, 0.0);
+    sp[1] = make_double2(0.0, 0.0);
   }
+  uint2 out;
+  if (cnt > 0) {
+    const float c = (float)cnt;
+    out.x = f32_to_bf16((float)s01.x / c) | ((uint32_t)f32_to_bf16((float)s01.y / c) << 16);
+    out.y = f32_to_bf16((float)s23.x / c) | ((uint32_t)f32_to_bf16((float)s23.y / c) << 16);
+  } else {
+    out = *(const uint2*)(old_c + i);
+  }
+  *(uint2*)(new_c + i) = out;
 }
 
 __global__ void zero_f64_kernel(double* __restrict__ p, long long n) {
@@ -233,7 +243,7 @@ int svoo_centroid_move_impl(const uint16_t* x, const int32_t* sorted_idx, const 
   hipLaunchKernelGGL(centroid_move_kernel, dim3(blocks), dim3(256), 0, stream, (const uint32_t*)x, sorted_idx,
                      sorted_labels, changes, nchanges, sums, sizes, n, k, limit, nbx, bh);
   const long long total = (long long)bh * k * 128;
-  const long long fthreads = max(total, zp ? zn : 0ll);
+  const long long fthreads = max(total / 4, zp ? zn : 0ll);
   hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((fthreads + 255) / 256)), dim3(256), 0, stream, sums,
                      sizes, old_c, new_c, total, 128, 1, nchanges, zp, zn);
   return check_launch("svoo_centroid_move");
@@ -250,7 +260,7 @@ int svoo_centroid_update_impl(const uint16_t* x, const int32_t* sorted_idx, cons
   hipLaunchKernelGGL(centroid_accumulate_kernel, grid, dim3(256), 0, stream, (const uint32_t*)x, sorted_idx,
                      sorted_labels, sums, n, k);
   const long long total = (long long)bh * k * 128;
-  const long long fthreads = max(total, zp ? zn : 0ll);
+  const long long fthreads = max(total / 4, zp ? zn : 0ll);
   hipLaunchKernelGGL(centroid_finalize_kernel, dim3((unsigned)((fthreads + 255) / 256)), dim3(256), 0, stream, sums,
                      sizes, old_c, new_c, total, 128, keep_sums, (int32_t*)nullptr, zp, zn);
   return check_launch("svoo_centroid_update");
