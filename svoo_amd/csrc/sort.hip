@@ -12,6 +12,8 @@
 //               original token order (stable).  A cluster's output lines collect one or two tokens
 //               from each of ~70 chunks (K = 1000, N = 75600): with a head's chunks on one XCD the
 //               4-byte writes merge in that XCD's L2 (81 -> 58 us per key-side sort at C3).
+// A launch of the three passes sorts the rows of one or two independent sorts (SortSide), so that the
+// co-clustering's two final sorts share their launches.
 #include "svoo_common.h"
 
 namespace svoo {
