@@ -86,6 +86,31 @@ def test_co_cluster_on_rounded_inputs(gpu, dtype):
     assert torch.equal(a["qlabels"], b["qlabels"]) and torch.equal(a["klabels"], b["klabels"])
 
 
+@pytest.mark.parametrize("n,qn,kn", [(30, 20, 8), (3000, 24, 80)])
+def test_co_cluster_final_sorts_are_stable_sorts_of_the_labels(gpu, n, qn, kn):
+    """The last step of the co-clustering sorts both sides' final labels: as one set of launches when the query
+    side's chunk counts fit the change list's buffer (n = 3000), one sort after the other when they do not
+    (n = 30).  Either way sizes, offsets and sorted indices are those of a stable sort of the returned labels."""
+    from svoo_amd.co_clustering import co_cluster_tokens_full
+
+    say("co_cluster final sorts", n, qn, kn)
+    bh = 2
+    q, k = _rand((bh, n, 128), torch.bfloat16, 11, gpu), _rand((bh, n, 128), torch.bfloat16, 12, gpu)
+    g = torch.Generator(device=gpu).manual_seed(7)
+    qi = torch.stack([torch.randperm(n, device=gpu, generator=g)[:qn] for _ in range(bh)])
+    ki = torch.stack([torch.randperm(n, device=gpu, generator=g)[:kn] for _ in range(bh)])
+    r = co_cluster_tokens_full(q, k, qn, kn, 3, init_q_idx=qi, init_k_idx=ki)
+    for side, c in (("q", qn), ("k", kn)):
+        lab = r[f"{side}labels"].cpu().numpy().astype(np.int64)
+        for b in range(bh):
+            sizes = np.bincount(lab[b], minlength=c)
+            np.testing.assert_array_equal(r[f"{side}sizes"][b].cpu().numpy(), sizes)
+            np.testing.assert_array_equal(r[f"{side}_offsets"][b].cpu().numpy(),
+                                          np.concatenate([[0], np.cumsum(sizes)[:-1]]))
+            np.testing.assert_array_equal(r[f"{side}_sorted_idx"][b].cpu().numpy(),
+                                          np.argsort(lab[b], kind="stable"))
+
+
 def _clusters(b, h, s, qn, kn, seed):
     r = np.random.default_rng(seed)
 
